@@ -1,0 +1,264 @@
+"""Benchmark of the routed-expert MoE layer on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config decode_t1]
+
+One step is one routed-expert MoE layer (route plan, fused gate/up FP8
+projection + SwiGLU, down FP8 projection + route weighting, route combine)
+over one batch of synthetic tokens, with every input already resident in HBM.
+All 256 experts of the layer are resident (9.7 GB of e4m3 bytes + scales) and
+every step uses a different routing drawn from 64 seeds, so consecutive steps
+touch different experts and the 256 MB Infinity Cache cannot hold the decode
+working set.
+
+Prints ONE JSON line: the headline metric (us per MoE layer of the
+``--config`` workload), the roofline of the dominant kernel (the fused gate/up
+projection: algorithmic bytes or flops per launch / its mean launch time from
+HIP events recorded on the launch stream), the CPU baseline (the numpy oracle
+on the host cores, a bounded sample), and secondary figures for the other
+configurations.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT / "glm-tpu_amd"))
+sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0
+ROTATIONS = 64
+TABLE_KEYS = ("gate_bits", "gate_scale", "up_bits", "up_scale", "down_bits", "down_scale")
+
+
+def parse_args():
+    p = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=100)
+    p.add_argument("--warmup", type=int, default=10)
+    p.add_argument("--config", default="decode_t1")
+    p.add_argument("--secondary", default="decode_t4,prefill_t2048,prefill_t8192_zipf",
+                   help="comma-separated extra configs measured after the headline ('' for none)")
+    p.add_argument("--secondary-steps", type=int, default=20)
+    p.add_argument("--no-cpu-baseline", action="store_true")
+    return p.parse_args()
+
+
+class Workload:
+    """Rotated synthetic routings of one config on the device, plus their costs."""
+
+    def __init__(self, cfg, tables, device, rotations=ROTATIONS, seed0=1000):
+        import torch
+
+        from glm_moe import synthetic as S
+
+        self.cfg = cfg
+        self.tables = tables
+        self.inputs = []
+        self.host = []
+        self.bytes_total, self.bytes_gate_up = [], []
+        for r in range(rotations):
+            seed = seed0 + r
+            ids, w = S.routes(cfg, seed)
+            x = S.hidden_states(cfg, seed)
+            xd = torch.from_numpy(x).to(torch.bfloat16).to(device)
+            self.inputs.append((xd, torch.from_numpy(ids).to(device), torch.from_numpy(w).to(device)))
+            self.host.append((x, ids, w))
+            b = S.algorithmic_bytes(cfg, ids)
+            self.bytes_total.append(b["total"])
+            self.bytes_gate_up.append(b["gate_up"])
+        self.flops = S.algorithmic_flops(cfg)
+
+
+def run_steps(work, steps, warmup, with_stage_events=True):
+    """Time `steps` layer calls; returns (ms per step, per-step stage timings)."""
+    import torch
+
+    from glm_moe.layers.moe.routed_experts import StageEvents, routed_experts
+
+    t = work.tables
+    tables = [t[k] for k in TABLE_KEYS]
+    out = torch.empty((work.cfg.tokens, work.cfg.hidden), dtype=torch.bfloat16, device=tables[0].device)
+    n_rot = len(work.inputs)
+    for i in range(warmup):
+        x, ids, w = work.inputs[i % n_rot]
+        routed_experts(x, ids, w, *tables, out=out)
+    events = [StageEvents() for _ in range(steps)] if with_stage_events else [None] * steps
+    start = torch.cuda.Event(enable_timing=True)
+    stop = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record()
+    for i in range(steps):
+        x, ids, w = work.inputs[(warmup + i) % n_rot]
+        routed_experts(x, ids, w, *tables, out=out, events=events[i])
+    stop.record()
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(stop) / steps
+    stages = []
+    if with_stage_events:
+        stages = [ev.elapsed() for ev in events]
+        for ev in events:
+            ev.close()
+    order = [(warmup + i) % n_rot for i in range(steps)]
+    return ms, stages, order
+
+
+def summarize(work, ms, stages, order):
+    gate_up_ms = np.array([s.gate_up for s in stages])
+    down_ms = np.array([s.down for s in stages])
+    plan_ms = np.array([s.plan for s in stages])
+    combine_ms = np.array([s.combine for s in stages])
+    bytes_total = np.array([work.bytes_total[i] for i in order], np.float64)
+    bytes_gu = np.array([work.bytes_gate_up[i] for i in order], np.float64)
+    return {
+        "us_per_layer": ms * 1e3,
+        "stage_us": {
+            "plan": float(plan_ms.mean() * 1e3),
+            "gate_up": float(gate_up_ms.mean() * 1e3),
+            "down": float(down_ms.mean() * 1e3),
+            "combine": float(combine_ms.mean() * 1e3),
+        },
+        "layer_hbm_gbs": float(bytes_total.mean() / (ms * 1e-3) / 1e9),
+        "gate_up_hbm_gbs": float(bytes_gu.mean() / (gate_up_ms.mean() * 1e-3) / 1e9),
+        "layer_tflops": float(work.flops["total"] / (ms * 1e-3) / 1e12),
+        "gate_up_tflops": float(work.flops["gate_up"] / (gate_up_ms.mean() * 1e-3) / 1e12),
+        "gate_up_bytes": float(bytes_gu.mean()),
+        "layer_bytes": float(bytes_total.mean()),
+        "distinct_experts": float(np.mean([len(np.unique(work.host[i][1])) for i in order])),
+    }
+
+
+def cpu_baseline(work, device):
+    """The numpy oracle on this host's cores, on one layer of the same workload."""
+    import torch
+
+    from oracle import moe_oracle as O
+
+    try:
+        from threadpoolctl import threadpool_info
+
+        blas_threads = max((p.get("num_threads", 1) for p in threadpool_info() if p.get("user_api") == "blas"),
+                           default=1)
+    except Exception:  # pragma: no cover - threadpoolctl missing
+        blas_threads = 1
+    x, ids, w = work.host[0]
+    used = np.unique(ids.reshape(-1))
+    index = torch.as_tensor(used, dtype=torch.long, device=device)
+    host = {k: work.tables[k].index_select(0, index).cpu().numpy() for k in TABLE_KEYS}
+    remap = np.searchsorted(used, ids).astype(np.int32)
+    tokens = ids.shape[0]
+    sample_tokens = tokens if tokens <= 4 else 4
+    times = []
+    budget_s = 20.0
+    t_all = time.perf_counter()
+    while len(times) < 3 and (time.perf_counter() - t_all) < budget_s:
+        t0 = time.perf_counter()
+        O.routed_experts(x[:sample_tokens], remap[:sample_tokens], w[:sample_tokens], **host)
+        times.append(time.perf_counter() - t0)
+    per_layer_us = float(np.median(times)) * 1e6 * (tokens / sample_tokens)
+    return {
+        "value": per_layer_us,
+        "unit": "us/layer",
+        "cores": int(blas_threads),
+        "kind": "port",
+        "sample": (f"numpy oracle (oracle/moe_oracle.py) on {sample_tokens} of {tokens} tokens of routing seed "
+                   f"{1000}, {len(used)} experts decoded per run, median of {len(times)} runs; elementwise "
+                   f"e4m3 decode single-threaded, FP32 BLAS on {blas_threads} threads"),
+    }
+
+
+def main():
+    args = parse_args()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this benchmark runs on one GPU only; the multi-GPU (expert-parallel) "
+                                   "design is documented, not measured", "n_gpus": args.gpus}))
+        sys.exit(2)
+    import torch
+
+    from glm_moe import synthetic as S
+
+    if not torch.cuda.is_available():
+        print(json.dumps({"error": "no GPU visible"}))
+        sys.exit(1)
+    device = torch.device("cuda:0")
+    cfg = S.CONFIGS[args.config]
+    print(f"[bench] generating {cfg.experts} experts of {cfg.name} weights on {device}", file=sys.stderr, flush=True)
+    tables = S.device_expert_tables(cfg, seed=0, device=device)
+    torch.cuda.synchronize()
+    work = Workload(cfg, tables, device)
+    print(f"[bench] timing {args.steps} steps after {args.warmup} warmups", file=sys.stderr, flush=True)
+    ms, stages, order = run_steps(work, args.steps, args.warmup)
+    head = summarize(work, ms, stages, order)
+
+    decode_like = cfg.tokens * cfg.top_k <= 8 * cfg.experts
+    if decode_like:
+        achieved = head["gate_up_bytes"] / (head["stage_us"]["gate_up"] * 1e-6) / 1e9
+        roofline = {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                    "frac": achieved / HBM_PEAK_GBS, "traffic": None, "kernel": "grouped_fp8_gemm gate/up+SwiGLU"}
+    else:
+        achieved = head["gate_up_tflops"]
+        roofline = {"bound": "mfma", "achieved": achieved, "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                    "frac": achieved / BF16_PEAK_TFLOPS, "traffic": None,
+                    "kernel": "grouped_fp8_gemm gate/up+SwiGLU"}
+
+    secondary = {}
+    for name in [s for s in args.secondary.split(",") if s]:
+        if name == cfg.name:
+            continue
+        scfg = S.CONFIGS[name]
+        print(f"[bench] secondary {name}", file=sys.stderr, flush=True)
+        swork = Workload(scfg, tables, device, rotations=8)
+        sms, sstages, sorder = run_steps(swork, args.secondary_steps, 3)
+        s = summarize(swork, sms, sstages, sorder)
+        s["hbm_frac"] = s["layer_hbm_gbs"] / HBM_PEAK_GBS
+        s["bf16_mfma_frac"] = s["layer_tflops"] / BF16_PEAK_TFLOPS
+        secondary[name] = s
+        del swork
+
+    baseline = None
+    if not args.no_cpu_baseline:
+        print("[bench] CPU baseline (numpy oracle)", file=sys.stderr, flush=True)
+        baseline = cpu_baseline(work, device)
+
+    line = {
+        "metric": "us per routed-expert MoE layer (decode T=1, E=256, H=6144, I=2048, top-8)"
+        if cfg.name == "decode_t1" else f"us per routed-expert MoE layer ({cfg.name})",
+        "value": head["us_per_layer"],
+        "unit": "us/layer",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms,
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) activations and router logits, N(0,0.02) e4m3fn weights with "
+                "128x128 FP32 block scales, generated on the GPU)",
+        "config": {
+            "workload": f"{cfg.name}: T={cfg.tokens} E={cfg.experts} H={cfg.hidden} I={cfg.intermediate} "
+                        f"top-{cfg.top_k}, all experts resident, {ROTATIONS} rotated routings",
+            "tokens": cfg.tokens, "experts": cfg.experts, "hidden": cfg.hidden,
+            "intermediate": cfg.intermediate, "top_k": cfg.top_k,
+        },
+        "layer_hbm_gbs": head["layer_hbm_gbs"],
+        "layer_hbm_frac": head["layer_hbm_gbs"] / HBM_PEAK_GBS,
+        "stage_us": head["stage_us"],
+        "distinct_experts": head["distinct_experts"],
+        "roofline": roofline,
+        "cpu_baseline": baseline,
+        "secondary": secondary,
+    }
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,270 @@
+// Row movement, FP8 table decode and the route combine of the MoE path.
+#include "moe_common.h"
+#include "moe_kernels.h"
+
+namespace glm_moe {
+
+namespace {
+
+// decode_fp8_table (reference glm_tpu/layers/fp8.py:113-126):
+// out[n][k] = bf16(f32(e4m3(bits[n][k])) * scale[n / bn][k / bk]).
+__global__ void decode_fp8_table_kernel(const uint8_t* bits, const float* scale, int64_t n, int64_t k,
+                                        int32_t bn, int32_t bk, uint16_t* out) {
+  const int64_t kblocks = (k + bk - 1) / bk;
+  const int64_t total = n * k;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t row = i / k;
+    const int64_t col = i - row * k;
+    const float s = scale[(row / bn) * kblocks + col / bk];
+    const float v = __builtin_amdgcn_cvt_pk_f32_fp8((uint32_t)bits[i], false)[0];
+    out[i] = f32_to_bf16_bits(v * s);
+  }
+}
+
+// dst[i] = mask[i] ? src[clamp(index[i], 0, src_rows - 1) / div] : 0, row-wise (dwords).
+__global__ void gather_rows_kernel(const uint32_t* src, int64_t src_rows, int64_t row_words,
+                                   const int32_t* index, int32_t div, const uint8_t* mask, int64_t n,
+                                   uint32_t* dst) {
+  const int64_t total = n * row_words;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t row = i / row_words;
+    const int64_t w = i - row * row_words;
+    const bool keep = mask == nullptr || mask[row] != 0;
+    uint32_t v = 0;
+    if (keep) {
+      int64_t s = index[row];
+      s = s < 0 ? 0 : (s >= src_rows ? src_rows - 1 : s);
+      s /= div;
+      v = src[s * row_words + w];
+    }
+    dst[i] = v;
+  }
+}
+
+// pack_expert_panel_rows (panels.py:86-95): [capacity, panel_rows, row] with
+// rows beyond a panel's live count zero.
+__global__ void pack_panel_rows_kernel(const uint32_t* src, int64_t src_rows, int64_t row_words,
+                                       const int32_t* row_starts, const int32_t* live_counts,
+                                       int32_t capacity, int32_t panel_rows, uint32_t* dst) {
+  const int64_t total = (int64_t)capacity * panel_rows * row_words;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t row = i / row_words;
+    const int64_t w = i - row * row_words;
+    const int p = (int)(row / panel_rows);
+    const int lane = (int)(row - (int64_t)p * panel_rows);
+    uint32_t v = 0;
+    if (lane < live_counts[p]) {
+      int64_t s = (int64_t)row_starts[p] + lane;
+      s = s < 0 ? 0 : (s >= src_rows ? src_rows - 1 : s);
+      v = src[s * row_words + w];
+    }
+    dst[i] = v;
+  }
+}
+
+// Zero every row whose keep flag is 0, or every row when *valid == 0.
+__global__ void zero_rows_kernel(uint32_t* out, int64_t rows, int64_t row_words, const uint8_t* keep,
+                                 const uint8_t* valid) {
+  const bool all = valid != nullptr && valid[0] == 0;
+  const int64_t total = rows * row_words;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t row = i / row_words;
+    if (all || (keep != nullptr && keep[row] == 0)) out[i] = 0u;
+  }
+}
+
+// FP32 sum of a token's top-k weighted route rows in slot order, one bf16
+// rounding (routed_experts.py:106-117); with bf16_sum the running sum is
+// rounded to bf16 after every slot instead (the decode body, :293).  With
+// ids given, a slot whose raw expert id lies outside [0, experts) is not
+// owned and contributes nothing (the decode ownership rule, :250-253).
+// y is [tokens * top_k, h] in flat (token, slot) order.  Eight columns per thread.
+__global__ void combine_routes_kernel(const uint16_t* y, int64_t tokens, int32_t top_k, int64_t h,
+                                      const int32_t* ids, int32_t experts, int32_t bf16_sum,
+                                      uint16_t* out) {
+  const int64_t groups = h / 8;
+  const int64_t total = tokens * groups;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t t = i / groups;
+    const int64_t c = (i - t * groups) * 8;
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    {
+      for (int s = 0; s < top_k; ++s) {
+        if (ids != nullptr) {
+          const int32_t id = ids[t * top_k + s];
+          if (id < 0 || id >= experts) continue;
+        }
+        const u32x4 v = *reinterpret_cast<const u32x4*>(y + ((t * top_k + s) * h + c));
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          acc[2 * j] += bf16_bits_to_f32(v[j] & 0xFFFFu);
+          acc[2 * j + 1] += bf16_bits_to_f32(v[j] >> 16);
+          if (bf16_sum) {
+            acc[2 * j] = round_to_bf16(acc[2 * j]);
+            acc[2 * j + 1] = round_to_bf16(acc[2 * j + 1]);
+          }
+        }
+      }
+    }
+    u32x4 o;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) o[j] = pack_bf16x2(acc[2 * j], acc[2 * j + 1]);
+    *reinterpret_cast<u32x4*>(out + t * h + c) = o;
+  }
+}
+
+__global__ void fill_u32_kernel(uint32_t* dst, int64_t words, uint32_t value) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < words;
+       i += (int64_t)gridDim.x * blockDim.x)
+    dst[i] = value;
+}
+
+
+// Synthetic FP8 expert weights for tests and benchmarks, the recipe of the
+// reference's fixture generator (tools/equivalence/fixture.py:158-172) with
+// per-block scales: w ~ N(0, sigma) from a counter-based hash (splitmix64
+// finaliser) and Box-Muller; per 128x128 block scale = amax / 448; bits =
+// e4m3fn(clamp(w / scale, +-448)) rounded to nearest even.  One workgroup per
+// block, 256 threads x 64 values (two threads per 128-byte row).
+__device__ __forceinline__ uint64_t splitmix64(uint64_t z) {
+  z += 0x9E3779B97F4A7C15ull;
+  z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+  z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+  return z ^ (z >> 31);
+}
+
+__global__ __launch_bounds__(256) void synth_fp8_kernel(uint64_t seed, int64_t n, int64_t k, float sigma,
+                                                        uint8_t* bits, float* scales) {
+  __shared__ float s_max[4];
+  const int64_t nb = n / 128, kb = k / 128;
+  const int64_t blk = blockIdx.x;
+  const int64_t e = blk / (nb * kb);
+  const int64_t rem = blk - e * nb * kb;
+  const int64_t bn = rem / kb, bk = rem - bn * kb;
+  const int tid = threadIdx.x;
+  const int64_t row = bn * 128 + (tid >> 1);
+  const int64_t col0 = bk * 128 + (tid & 1) * 64;
+  const int64_t elem0 = (e * n + row) * k + col0;
+  float v[64];
+  float m = 0.0f;
+#pragma unroll
+  for (int j = 0; j < 64; j += 2) {
+    const uint64_t h = splitmix64(seed ^ splitmix64((uint64_t)(elem0 + j)));
+    const float u1 = ((uint32_t)(h >> 40) + 1.0f) * (1.0f / 16777217.0f);  // (0, 1]
+    const float u2 = (uint32_t)(h & 0xFFFFFFu) * (1.0f / 16777216.0f);     // [0, 1)
+    const float r = sigma * sqrtf(-2.0f * __logf(u1));
+    float sn, cs;
+    __sincosf(6.283185307179586f * u2, &sn, &cs);
+    v[j] = r * cs;
+    v[j + 1] = r * sn;
+    m = fmaxf(m, fmaxf(fabsf(v[j]), fabsf(v[j + 1])));
+  }
+  for (int d = 32; d > 0; d >>= 1) m = fmaxf(m, __shfl_xor(m, d, 64));
+  if ((tid & 63) == 0) s_max[tid >> 6] = m;
+  __syncthreads();
+  const float amax = fmaxf(fmaxf(s_max[0], s_max[1]), fmaxf(s_max[2], s_max[3]));
+  const float scale = amax > 0.0f ? amax / 448.0f : 1.0f;
+  if (tid == 0) scales[(e * nb + bn) * kb + bk] = scale;
+  u32x4 out[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      const int j = q * 16 + w * 4;
+      float a0 = fminf(fmaxf(v[j] / scale, -448.0f), 448.0f);
+      float a1 = fminf(fmaxf(v[j + 1] / scale, -448.0f), 448.0f);
+      float a2 = fminf(fmaxf(v[j + 2] / scale, -448.0f), 448.0f);
+      float a3 = fminf(fmaxf(v[j + 3] / scale, -448.0f), 448.0f);
+      int packed = __builtin_amdgcn_cvt_pk_fp8_f32(a0, a1, 0, false);
+      packed = __builtin_amdgcn_cvt_pk_fp8_f32(a2, a3, packed, true);
+      out[q][w] = (uint32_t)packed;
+    }
+  }
+  u32x4* dst = reinterpret_cast<u32x4*>(bits + elem0);
+#pragma unroll
+  for (int q = 0; q < 4; ++q) dst[q] = out[q];
+}
+
+dim3 grid_for(int64_t work, int threads) {
+  int64_t blocks = (work + threads - 1) / threads;
+  if (blocks < 1) blocks = 1;
+  if (blocks > 65536) blocks = 65536;
+  return dim3((unsigned)blocks);
+}
+
+}  // namespace
+
+hipError_t launch_synth_fp8(uint64_t seed, int32_t experts, int64_t n, int64_t k, float sigma,
+                            uint8_t* bits, float* scales, hipStream_t stream) {
+  const int64_t blocks = (int64_t)experts * (n / 128) * (k / 128);
+  if (blocks == 0) return hipSuccess;
+  hipLaunchKernelGGL(synth_fp8_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, seed, n, k, sigma,
+                     bits, scales);
+  return hipGetLastError();
+}
+
+hipError_t launch_decode_fp8_table(const uint8_t* bits, const float* scale, int64_t n, int64_t k,
+                                   int32_t block_n, int32_t block_k, uint16_t* out,
+                                   hipStream_t stream) {
+  if (n * k == 0) return hipSuccess;
+  hipLaunchKernelGGL(decode_fp8_table_kernel, grid_for(n * k, 256), dim3(256), 0, stream, bits, scale,
+                     n, k, block_n, block_k, out);
+  return hipGetLastError();
+}
+
+hipError_t launch_gather_rows(const void* src, int64_t src_rows, int64_t row_bytes,
+                              const int32_t* index, int32_t div, const uint8_t* mask, int64_t n,
+                              void* dst, hipStream_t stream) {
+  const int64_t words = row_bytes / 4;
+  if (n * words == 0) return hipSuccess;
+  hipLaunchKernelGGL(gather_rows_kernel, grid_for(n * words, 256), dim3(256), 0, stream,
+                     static_cast<const uint32_t*>(src), src_rows, words, index, div, mask, n,
+                     static_cast<uint32_t*>(dst));
+  return hipGetLastError();
+}
+
+hipError_t launch_pack_panel_rows(const void* src, int64_t src_rows, int64_t row_bytes,
+                                  const int32_t* row_starts, const int32_t* live_counts,
+                                  int32_t capacity, int32_t panel_rows, void* dst,
+                                  hipStream_t stream) {
+  const int64_t words = row_bytes / 4;
+  const int64_t total = (int64_t)capacity * panel_rows * words;
+  if (total == 0) return hipSuccess;
+  hipLaunchKernelGGL(pack_panel_rows_kernel, grid_for(total, 256), dim3(256), 0, stream,
+                     static_cast<const uint32_t*>(src), src_rows, words, row_starts, live_counts,
+                     capacity, panel_rows, static_cast<uint32_t*>(dst));
+  return hipGetLastError();
+}
+
+hipError_t launch_zero_rows(void* out, int64_t rows, int64_t row_bytes, const uint8_t* keep,
+                            const uint8_t* valid, hipStream_t stream) {
+  const int64_t words = row_bytes / 4;
+  if (rows * words == 0) return hipSuccess;
+  hipLaunchKernelGGL(zero_rows_kernel, grid_for(rows * words, 256), dim3(256), 0, stream,
+                     static_cast<uint32_t*>(out), rows, words, keep, valid);
+  return hipGetLastError();
+}
+
+hipError_t launch_combine_routes(const uint16_t* y, int64_t tokens, int32_t top_k, int64_t h,
+                                 const int32_t* ids, int32_t experts, int32_t bf16_sum,
+                                 uint16_t* out, hipStream_t stream) {
+  const int64_t total = tokens * (h / 8);
+  if (total == 0) return hipSuccess;
+  hipLaunchKernelGGL(combine_routes_kernel, grid_for(total, 256), dim3(256), 0, stream, y, tokens,
+                     top_k, h, ids, experts, bf16_sum, out);
+  return hipGetLastError();
+}
+
+hipError_t launch_fill_u32(void* dst, int64_t words, uint32_t value, hipStream_t stream) {
+  if (words == 0) return hipSuccess;
+  hipLaunchKernelGGL(fill_u32_kernel, grid_for(words, 256), dim3(256), 0, stream,
+                     static_cast<uint32_t*>(dst), words, value);
+  return hipGetLastError();
+}
+
+}  // namespace glm_moe

@@ -1,0 +1,490 @@
+// extern "C" entry points of libglm_moe.so (declared in include/glm_moe.h).
+//
+// Static geometry checks mirror the reference's trace-time ValueErrors; the
+// kernels never see a shape they were not built for.  Nothing here allocates.
+#include <stdarg.h>
+#include <stdio.h>
+
+#include <string>
+
+#include "../../include/glm_moe.h"
+#include "moe_common.h"
+#include "moe_kernels.h"
+
+using namespace glm_moe;
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int status, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+  return status;
+}
+
+int check_hip(hipError_t err, const char* what) {
+  if (err == hipSuccess) return GLM_MOE_OK;
+  return fail(GLM_MOE_ERR_DEVICE, "%s: %s", what, hipGetErrorString(err));
+}
+
+#define GLM_REQUIRE(cond, ...) \
+  do {                         \
+    if (!(cond)) return fail(GLM_MOE_ERR_ARGUMENT, __VA_ARGS__); \
+  } while (0)
+
+#define GLM_HIP(call, what)                        \
+  do {                                             \
+    const int _st = check_hip((call), (what));     \
+    if (_st != GLM_MOE_OK) return _st;             \
+  } while (0)
+
+constexpr size_t kAlign = 256;
+
+size_t align_up(size_t v) { return (v + kAlign - 1) & ~(kAlign - 1); }
+
+int key_bits_for(int experts) {
+  int bits = 0;
+  while ((1 << bits) < experts) ++bits;
+  return bits;
+}
+
+// Shape family of the grouped GEMM for a route set: the skinny split-K kernel
+// while experts see few routes each (decode), the wide one otherwise.
+int routed_shape(int64_t routes, int32_t experts) {
+  return routes <= 8 * (int64_t)experts ? kShapeSkinny : kShapeWide;
+}
+
+int64_t max_tiles_for(int64_t routes, int32_t experts, int rows) {
+  return (routes + rows - 1) / rows + (routes < experts ? routes : experts);
+}
+
+// Byte layout of the glm_moe_routed_experts workspace.
+struct RoutedLayout {
+  size_t sorted, inverse, counts, offsets, tiles, act, y, total;
+  int64_t max_tiles;
+};
+
+RoutedLayout routed_layout(int64_t tokens, int32_t top_k, int32_t experts, int64_t hidden,
+                           int64_t intermediate) {
+  RoutedLayout L{};
+  const int64_t n = tokens * top_k;
+  const int shape = routed_shape(n, experts);
+  L.max_tiles = max_tiles_for(n, experts, gemm_shape_rows(shape));
+  size_t off = 0;
+  L.sorted = off;  off = align_up(off + sizeof(int32_t) * n);
+  L.inverse = off; off = align_up(off + sizeof(int32_t) * n);
+  L.counts = off;  off = align_up(off + sizeof(int32_t) * experts);
+  L.offsets = off; off = align_up(off + sizeof(int32_t) * (experts + 1));
+  L.tiles = off;   off = align_up(off + sizeof(int32_t) * (3 * L.max_tiles + 1));
+  L.act = off;     off = align_up(off + sizeof(uint16_t) * n * intermediate);
+  L.y = off;       off = align_up(off + sizeof(uint16_t) * n * hidden);
+  L.total = off;
+  return L;
+}
+
+hipStream_t as_stream(void* s) { return static_cast<hipStream_t>(s); }
+
+int record(void* const* events, int i, hipStream_t stream) {
+  if (events == nullptr) return GLM_MOE_OK;
+  return check_hip(hipEventRecord(static_cast<hipEvent_t>(events[i]), stream), "hipEventRecord");
+}
+
+int routed_experts_impl(const uint16_t* hidden, int64_t tokens, int64_t hidden_size,
+                        const int32_t* route_indices, const float* route_weights, int32_t top_k,
+                        int32_t num_experts, int64_t intermediate, const uint8_t* gate_bits,
+                        const float* gate_scale, const uint8_t* up_bits, const float* up_scale,
+                        const uint8_t* down_bits, const float* down_scale, uint32_t flags,
+                        uint16_t* out, uint8_t* valid, void* workspace, size_t workspace_bytes,
+                        void* const* events, void* stream_ptr) {
+  GLM_REQUIRE(tokens > 0 && top_k > 0 && num_experts > 0, "routed experts need tokens, top_k, experts > 0");
+  GLM_REQUIRE(top_k <= num_experts, "top_k exceeds expert count");
+  GLM_REQUIRE(num_experts <= kMaxExperts, "at most %d experts", kMaxExperts);
+  GLM_REQUIRE(tokens * top_k <= INT32_MAX / 2, "too many routes");
+  GLM_REQUIRE(hidden_size > 0 && hidden_size % 128 == 0, "hidden size must be a positive multiple of 128");
+  GLM_REQUIRE(intermediate > 0 && intermediate % 128 == 0, "intermediate size must be a positive multiple of 128");
+  GLM_REQUIRE(hidden_size <= INT32_MAX / 2 && intermediate <= INT32_MAX / 2, "dimension too large");
+  GLM_REQUIRE(hidden && route_indices && route_weights && gate_bits && gate_scale && up_bits &&
+                  up_scale && down_bits && down_scale && out && valid,
+              "null tensor pointer");
+  const int64_t n = tokens * top_k;
+  const int shape = routed_shape(n, num_experts);
+  const int bn13 = gemm_shape_bn(shape, 2);
+  const int bn2 = gemm_shape_bn(shape, 1);
+  GLM_REQUIRE(intermediate % bn13 == 0, "intermediate size must be a multiple of %d", bn13);
+  GLM_REQUIRE(hidden_size % bn2 == 0, "hidden size must be a multiple of %d", bn2);
+  const RoutedLayout L = routed_layout(tokens, top_k, num_experts, hidden_size, intermediate);
+  if (workspace_bytes < L.total || workspace == nullptr)
+    return fail(GLM_MOE_ERR_WORKSPACE, "workspace of %zu bytes needed, %zu given", L.total, workspace_bytes);
+  hipStream_t stream = as_stream(stream_ptr);
+  char* ws = static_cast<char*>(workspace);
+  int32_t* sorted = reinterpret_cast<int32_t*>(ws + L.sorted);
+  int32_t* inverse = reinterpret_cast<int32_t*>(ws + L.inverse);
+  int32_t* counts = reinterpret_cast<int32_t*>(ws + L.counts);
+  int32_t* offsets = reinterpret_cast<int32_t*>(ws + L.offsets);
+  int32_t* tile_expert = reinterpret_cast<int32_t*>(ws + L.tiles);
+  int32_t* tile_row = tile_expert + L.max_tiles;
+  int32_t* tile_live = tile_row + L.max_tiles;
+  int32_t* tile_count = tile_live + L.max_tiles;
+  uint16_t* act = reinterpret_cast<uint16_t*>(ws + L.act);
+  uint16_t* y = reinterpret_cast<uint16_t*>(ws + L.y);
+
+  int st = record(events, 0, stream);
+  if (st) return st;
+
+  RoutePlanArgs p{};
+  p.ids = route_indices;
+  p.n = (int32_t)n;
+  p.top_k = top_k;
+  p.experts = num_experts;
+  p.key_bits = key_bits_for(num_experts);
+  p.route_w = (flags & GLM_MOE_CHECK_WEIGHTS) ? route_weights : nullptr;
+  p.sorted = sorted;
+  p.inverse = inverse;
+  p.counts = counts;
+  p.offsets = offsets;
+  p.valid = valid;
+  p.tile_rows = gemm_shape_rows(shape);
+  p.max_tiles = (int32_t)L.max_tiles;
+  p.tile_expert = tile_expert;
+  p.tile_row = tile_row;
+  p.tile_live = tile_live;
+  p.tile_count = tile_count;
+  GLM_HIP(launch_route_plan(p, stream), "route plan launch");
+  if ((st = record(events, 1, stream))) return st;
+
+  // Every route (with its safe id) is covered by exactly one tile, so every
+  // row of act and y is written before it is read.
+  GroupedGemmArgs g{};
+  g.experts = num_experts;
+  g.rows = (int32_t)n;
+  g.x_rows = tokens;
+  g.out_rows = n;
+  g.x = hidden;
+  g.x_row_ids = sorted;
+  g.x_row_div = top_k;
+  g.w0 = gate_bits;
+  g.s0 = gate_scale;
+  g.w1 = up_bits;
+  g.s1 = up_scale;
+  g.n = (int32_t)intermediate;
+  g.k = (int32_t)hidden_size;
+  g.tile_expert = tile_expert;
+  g.tile_row = tile_row;
+  g.tile_live = tile_live;
+  g.tile_count = tile_count;
+  g.max_tiles = (int32_t)L.max_tiles;
+  g.valid = nullptr;
+  g.out = act;
+  g.ldo = intermediate;
+  g.table_stride = 0;
+  g.out_row_ids = nullptr;
+  g.route_w = nullptr;
+  GLM_HIP(launch_grouped_gemm(g, shape, 2, kEpiSwiglu, stream), "gate/up launch");
+  if ((st = record(events, 2, stream))) return st;
+
+  GroupedGemmArgs d{};
+  d.experts = num_experts;
+  d.rows = (int32_t)n;
+  d.x_rows = n;
+  d.out_rows = n;
+  d.x = act;
+  d.x_row_ids = nullptr;
+  d.x_row_div = 1;
+  d.w0 = down_bits;
+  d.s0 = down_scale;
+  d.n = (int32_t)hidden_size;
+  d.k = (int32_t)intermediate;
+  d.tile_expert = tile_expert;
+  d.tile_row = tile_row;
+  d.tile_live = tile_live;
+  d.tile_count = tile_count;
+  d.max_tiles = (int32_t)L.max_tiles;
+  d.valid = nullptr;
+  d.out = y;
+  d.ldo = hidden_size;
+  d.table_stride = 0;
+  d.out_row_ids = sorted;
+  d.route_w = route_weights;
+  GLM_HIP(launch_grouped_gemm(d, shape, 1, kEpiWeighted, stream), "down launch");
+  if ((st = record(events, 3, stream))) return st;
+
+  GLM_HIP(launch_combine_routes(y, tokens, top_k, hidden_size,
+                                (flags & GLM_MOE_DROP_UNOWNED) ? route_indices : nullptr, num_experts,
+                                (flags & GLM_MOE_ROUTE_SUM_BF16) ? 1 : 0, out, stream),
+          "combine launch");
+  return record(events, 4, stream);
+}
+
+}  // namespace
+
+extern "C" {
+
+int glm_moe_abi_version(void) { return GLM_MOE_ABI_VERSION; }
+
+const char* glm_moe_last_error(void) { return g_last_error.c_str(); }
+
+int glm_moe_decode_fp8_table(const uint8_t* bits, const float* scale, int64_t n, int64_t k,
+                             int32_t block_n, int32_t block_k, uint16_t* out_bf16, void* stream) {
+  GLM_REQUIRE(n >= 0 && k >= 0, "negative table shape");
+  GLM_REQUIRE(block_n > 0 && block_k > 0, "block_shape must contain two positive integers");
+  GLM_REQUIRE((n == 0 || k == 0) || (bits && scale && out_bf16), "null tensor pointer");
+  GLM_HIP(launch_decode_fp8_table(bits, scale, n, k, block_n, block_k, out_bf16, as_stream(stream)),
+          "decode launch");
+  return GLM_MOE_OK;
+}
+
+int glm_moe_group_routes(const int32_t* route_indices, int64_t tokens, int32_t top_k,
+                         int32_t num_experts, int32_t* sorted_flat_ids,
+                         int32_t* inverse_permutation, int32_t* group_sizes, uint8_t* valid,
+                         void* stream) {
+  GLM_REQUIRE(tokens > 0 && top_k > 0, "routes must be nonempty [tokens,top_k]");
+  GLM_REQUIRE(num_experts > 0, "num_experts must be a positive integer");
+  GLM_REQUIRE(top_k <= num_experts, "top_k exceeds expert count");
+  GLM_REQUIRE(num_experts <= kMaxExperts, "at most %d experts", kMaxExperts);
+  GLM_REQUIRE(tokens * top_k <= INT32_MAX / 2, "too many routes");
+  GLM_REQUIRE(route_indices && sorted_flat_ids && inverse_permutation && group_sizes && valid,
+              "null tensor pointer");
+  RoutePlanArgs p{};
+  p.ids = route_indices;
+  p.n = (int32_t)(tokens * top_k);
+  p.top_k = top_k;
+  p.experts = num_experts;
+  p.key_bits = key_bits_for(num_experts);
+  p.sorted = sorted_flat_ids;
+  p.inverse = inverse_permutation;
+  p.counts = group_sizes;
+  p.valid = valid;
+  GLM_HIP(launch_route_plan(p, as_stream(stream)), "route plan launch");
+  return GLM_MOE_OK;
+}
+
+int glm_moe_gather_rows(const void* src, int64_t src_rows, int64_t row_bytes,
+                        const int32_t* index, int32_t div, const uint8_t* mask, int64_t rows,
+                        void* dst, void* stream) {
+  GLM_REQUIRE(rows >= 0 && row_bytes >= 0 && src_rows >= 0, "negative geometry");
+  GLM_REQUIRE(row_bytes % 4 == 0, "row bytes must be a multiple of 4");
+  GLM_REQUIRE(div > 0, "divisor must be positive");
+  if (rows == 0 || row_bytes == 0) return GLM_MOE_OK;
+  GLM_REQUIRE(src_rows > 0, "gather from an empty source");
+  GLM_REQUIRE(src && index && dst, "null tensor pointer");
+  GLM_HIP(launch_gather_rows(src, src_rows, row_bytes, index, div, mask, rows, dst, as_stream(stream)),
+          "gather launch");
+  return GLM_MOE_OK;
+}
+
+int glm_moe_build_expert_panels(const int32_t* group_sizes, int32_t num_groups,
+                                const int32_t* group_offset, int32_t rows, int32_t local_groups,
+                                int32_t* expert_ids, int32_t* row_starts, int32_t* live_counts,
+                                int32_t* active_panels, int32_t* restore_indices,
+                                uint8_t* owned_rows, uint8_t* valid, void* stream) {
+  GLM_REQUIRE(rows > 0 && local_groups > 0, "expert panels require bounded rows and int32 group counts");
+  GLM_REQUIRE(num_groups >= local_groups, "expert panels require bounded rows and int32 group counts");
+  GLM_REQUIRE((int64_t)(rows + 31) * num_groups <= INT32_MAX, "expert panels require bounded rows and int32 group counts");
+  GLM_REQUIRE(num_groups <= kMaxExperts, "at most %d groups", kMaxExperts);
+  GLM_REQUIRE(group_sizes && group_offset && expert_ids && row_starts && live_counts && active_panels &&
+                  restore_indices && owned_rows && valid,
+              "null tensor pointer");
+  PanelPlanArgs p{};
+  p.group_sizes = group_sizes;
+  p.groups = num_groups;
+  p.group_offset = group_offset;
+  p.rows = rows;
+  p.local_groups = local_groups;
+  p.panel_rows = 32;
+  p.capacity = (rows + 31) / 32 + local_groups - 1;
+  p.expert_ids = expert_ids;
+  p.row_starts = row_starts;
+  p.live_counts = live_counts;
+  p.active_panels = active_panels;
+  p.restore_indices = restore_indices;
+  p.owned_rows = owned_rows;
+  p.valid = valid;
+  GLM_HIP(launch_panel_plan(p, as_stream(stream)), "panel plan launch");
+  return GLM_MOE_OK;
+}
+
+int glm_moe_pack_expert_panel_rows(const void* values, int64_t rows, int64_t row_bytes,
+                                   const int32_t* row_starts, const int32_t* live_counts,
+                                   int32_t capacity, void* out, void* stream) {
+  GLM_REQUIRE(rows > 0 && capacity >= 0 && row_bytes >= 0, "panel packing row geometry disagrees");
+  GLM_REQUIRE(row_bytes % 4 == 0, "row bytes must be a multiple of 4");
+  if (capacity == 0 || row_bytes == 0) return GLM_MOE_OK;
+  GLM_REQUIRE(values && row_starts && live_counts && out, "null tensor pointer");
+  GLM_HIP(launch_pack_panel_rows(values, rows, row_bytes, row_starts, live_counts, capacity, 32, out,
+                                 as_stream(stream)),
+          "pack launch");
+  return GLM_MOE_OK;
+}
+
+int glm_moe_panel_fp8_matmul(const uint16_t* lhs, int64_t m, int64_t k, const uint8_t* weight_bits,
+                             const float* scale, int32_t groups, int64_t n,
+                             const int32_t* panel_expert_ids, const int32_t* panel_row_starts,
+                             const int32_t* panel_live_counts, const int32_t* active_panels,
+                             int32_t capacity, const uint8_t* owned_rows, const uint8_t* valid,
+                             int32_t result_dtype, void* out, void* stream) {
+  GLM_REQUIRE(m > 0 && k > 0 && groups > 0 && n > 0, "panel FP8 geometry/dtypes disagree with M32/N256/K128");
+  GLM_REQUIRE(k % 128 == 0 && n % 256 == 0 && n / 128 <= 128, "panel FP8 geometry/dtypes disagree with M32/N256/K128");
+  GLM_REQUIRE(capacity == (m + 31) / 32 + groups - 1, "panel FP8 geometry/dtypes disagree with M32/N256/K128");
+  GLM_REQUIRE(result_dtype == GLM_MOE_F32 || result_dtype == GLM_MOE_BF16, "result must be FP32 or BF16");
+  GLM_REQUIRE(k <= INT32_MAX / 2 && n <= INT32_MAX / 2 && m <= INT32_MAX / 2, "dimension too large");
+  GLM_REQUIRE(lhs && weight_bits && scale && panel_expert_ids && panel_row_starts && panel_live_counts &&
+                  active_panels && owned_rows && valid && out,
+              "null tensor pointer");
+  hipStream_t s = as_stream(stream);
+  const int64_t elem = result_dtype == GLM_MOE_F32 ? 4 : 2;
+  GLM_HIP(launch_zero_rows(out, m, n * elem, owned_rows, valid, s), "zero launch");
+  GroupedGemmArgs g{};
+  g.experts = groups;
+  g.rows = (int32_t)m;
+  g.x_rows = m;
+  g.out_rows = m;
+  g.x = lhs;
+  g.x_row_div = 1;
+  g.w0 = weight_bits;
+  g.s0 = scale;
+  g.n = (int32_t)n;
+  g.k = (int32_t)k;
+  g.tile_expert = panel_expert_ids;
+  g.tile_row = panel_row_starts;
+  g.tile_live = panel_live_counts;
+  g.tile_count = active_panels;
+  g.max_tiles = capacity;
+  g.valid = valid;
+  g.out = out;
+  g.ldo = n;
+  g.table_stride = 0;
+  GLM_HIP(launch_grouped_gemm(g, kShapePanel32, 1, result_dtype == GLM_MOE_F32 ? kEpiStoreF32 : kEpiStoreBf16, s),
+          "panel matmul launch");
+  return GLM_MOE_OK;
+}
+
+size_t glm_moe_routed_projection_workspace_bytes(int32_t slots) {
+  return align_up(sizeof(int32_t) * (3 * (size_t)(slots > 0 ? slots : 0) + 1));
+}
+
+int glm_moe_routed_projection(const uint16_t* lhs, int32_t slots, int64_t k, int32_t tables,
+                              const uint8_t* bits0, const float* scale0, const uint8_t* bits1,
+                              const float* scale1, int32_t experts, int64_t n,
+                              const int32_t* local_expert_ids, const uint8_t* owned,
+                              int32_t result_dtype, void* out, void* workspace,
+                              size_t workspace_bytes, void* stream) {
+  GLM_REQUIRE(tables == 1 || tables == 2, "routed FP8 projection takes one or two weight table pairs");
+  GLM_REQUIRE(slots > 0 && k > 0, "routed FP8 lhs dimensions must be positive");
+  GLM_REQUIRE(experts > 0 && n > 0, "routed FP8 weight/input geometry disagrees");
+  GLM_REQUIRE(k % 128 == 0 && n % 128 == 0, "routed FP8 requires N/K divisible by the scale block");
+  GLM_REQUIRE(result_dtype == GLM_MOE_F32 || result_dtype == GLM_MOE_BF16, "routed FP8 result must be FP32 or BF16");
+  GLM_REQUIRE(k <= INT32_MAX / 2 && n <= INT32_MAX / 2, "dimension too large");
+  GLM_REQUIRE(lhs && bits0 && scale0 && local_expert_ids && owned && out, "null tensor pointer");
+  GLM_REQUIRE(tables == 1 || (bits1 && scale1), "null tensor pointer");
+  if (workspace_bytes < glm_moe_routed_projection_workspace_bytes(slots) || workspace == nullptr)
+    return fail(GLM_MOE_ERR_WORKSPACE, "workspace of %zu bytes needed, %zu given",
+                glm_moe_routed_projection_workspace_bytes(slots), workspace_bytes);
+  hipStream_t s = as_stream(stream);
+  int32_t* tile_expert = static_cast<int32_t*>(workspace);
+  int32_t* tile_row = tile_expert + slots;
+  int32_t* tile_live = tile_row + slots;
+  int32_t* tile_count = tile_live + slots;
+  const int64_t elem = result_dtype == GLM_MOE_F32 ? 4 : 2;
+  GLM_HIP(launch_fill_u32(out, (int64_t)slots * tables * n * elem / 4, 0u, s), "zero launch");
+  GLM_HIP(launch_slot_tiles(local_expert_ids, owned, slots, experts, tile_expert, tile_row, tile_live,
+                            tile_count, s),
+          "slot plan launch");
+  GroupedGemmArgs g{};
+  g.experts = experts;
+  g.rows = slots;
+  g.x_rows = slots;
+  g.out_rows = slots;
+  g.x = lhs;
+  g.x_row_div = 1;
+  g.w0 = bits0;
+  g.s0 = scale0;
+  g.w1 = tables == 2 ? bits1 : nullptr;
+  g.s1 = tables == 2 ? scale1 : nullptr;
+  g.n = (int32_t)n;
+  g.k = (int32_t)k;
+  g.tile_expert = tile_expert;
+  g.tile_row = tile_row;
+  g.tile_live = tile_live;
+  g.tile_count = tile_count;
+  g.max_tiles = slots;
+  g.out = out;
+  g.ldo = (int64_t)tables * n;
+  g.table_stride = n;
+  GLM_HIP(launch_grouped_gemm(g, kShapeSkinny, tables, result_dtype == GLM_MOE_F32 ? kEpiStoreF32 : kEpiStoreBf16, s),
+          "routed projection launch");
+  return GLM_MOE_OK;
+}
+
+size_t glm_moe_routed_experts_workspace_bytes(int64_t tokens, int32_t top_k, int32_t num_experts,
+                                              int64_t hidden, int64_t intermediate) {
+  if (tokens <= 0 || top_k <= 0 || num_experts <= 0 || hidden <= 0 || intermediate <= 0) return 0;
+  return routed_layout(tokens, top_k, num_experts, hidden, intermediate).total;
+}
+
+int glm_moe_routed_experts(const uint16_t* hidden, int64_t tokens, int64_t hidden_size,
+                           const int32_t* route_indices, const float* route_weights,
+                           int32_t top_k, int32_t num_experts, int64_t intermediate,
+                           const uint8_t* gate_bits, const float* gate_scale,
+                           const uint8_t* up_bits, const float* up_scale,
+                           const uint8_t* down_bits, const float* down_scale, uint32_t flags,
+                           uint16_t* out, uint8_t* valid, void* workspace, size_t workspace_bytes,
+                           void* stream) {
+  return routed_experts_impl(hidden, tokens, hidden_size, route_indices, route_weights, top_k,
+                             num_experts, intermediate, gate_bits, gate_scale, up_bits, up_scale,
+                             down_bits, down_scale, flags, out, valid, workspace, workspace_bytes,
+                             nullptr, stream);
+}
+
+int glm_moe_routed_experts_timed(const uint16_t* hidden, int64_t tokens, int64_t hidden_size,
+                                 const int32_t* route_indices, const float* route_weights,
+                                 int32_t top_k, int32_t num_experts, int64_t intermediate,
+                                 const uint8_t* gate_bits, const float* gate_scale,
+                                 const uint8_t* up_bits, const float* up_scale,
+                                 const uint8_t* down_bits, const float* down_scale,
+                                 uint32_t flags, uint16_t* out, uint8_t* valid, void* workspace,
+                                 size_t workspace_bytes, void* const* events, void* stream) {
+  GLM_REQUIRE(events != nullptr, "five events required");
+  for (int i = 0; i < 5; ++i) GLM_REQUIRE(events[i] != nullptr, "five events required");
+  return routed_experts_impl(hidden, tokens, hidden_size, route_indices, route_weights, top_k,
+                             num_experts, intermediate, gate_bits, gate_scale, up_bits, up_scale,
+                             down_bits, down_scale, flags, out, valid, workspace, workspace_bytes,
+                             events, stream);
+}
+
+int glm_moe_event_create(void** event) {
+  GLM_REQUIRE(event != nullptr, "null event slot");
+  hipEvent_t e = nullptr;
+  GLM_HIP(hipEventCreate(&e), "hipEventCreate");
+  *event = e;
+  return GLM_MOE_OK;
+}
+
+int glm_moe_event_destroy(void* event) {
+  if (event == nullptr) return GLM_MOE_OK;
+  GLM_HIP(hipEventDestroy(static_cast<hipEvent_t>(event)), "hipEventDestroy");
+  return GLM_MOE_OK;
+}
+
+int glm_moe_event_elapsed_ms(void* start, void* stop, float* ms) {
+  GLM_REQUIRE(start && stop && ms, "null event");
+  GLM_HIP(hipEventElapsedTime(ms, static_cast<hipEvent_t>(start), static_cast<hipEvent_t>(stop)),
+          "hipEventElapsedTime");
+  return GLM_MOE_OK;
+}
+
+int glm_moe_synthesize_fp8_weights(uint64_t seed, int32_t experts, int64_t n, int64_t k, float sigma,
+                                   uint8_t* bits, float* scales, void* stream) {
+  GLM_REQUIRE(experts > 0 && n > 0 && k > 0, "synthetic weights need positive geometry");
+  GLM_REQUIRE(n % 128 == 0 && k % 128 == 0, "synthetic weights need N and K multiples of 128");
+  GLM_REQUIRE(sigma > 0.0f, "sigma must be positive");
+  GLM_REQUIRE(bits && scales, "null tensor pointer");
+  GLM_HIP(launch_synth_fp8(seed, experts, n, k, sigma, bits, scales, as_stream(stream)), "synth launch");
+  return GLM_MOE_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,77 @@
+// Shared device helpers of the routed-expert MoE library (gfx950 / CDNA4).
+//
+// Numerics follow glm-tpu's FP8 block decode: an e4m3fn byte is decoded
+// exactly to FP32, multiplied by its FP32 128x128 block scale in FP32 and
+// rounded once (RNE) to bf16 (reference glm_tpu/layers/fp8.py:113-126).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace glm_moe {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+constexpr int kScaleBlock = 128;  // checkpoint scale block along N and K
+constexpr int kWave = 64;
+
+__device__ __forceinline__ float bf16_bits_to_f32(uint32_t bits16) {
+  return __uint_as_float(bits16 << 16);
+}
+
+// RNE float -> bf16 bits (v_cvt_pk_bf16_f32 on gfx950; NaN stays NaN).
+__device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
+  __bf16 h = (__bf16)f;
+  return __builtin_bit_cast(uint16_t, h);
+}
+
+__device__ __forceinline__ float round_to_bf16(float f) {
+  return bf16_bits_to_f32(f32_to_bf16_bits(f));
+}
+
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  return (uint32_t)f32_to_bf16_bits(lo) | ((uint32_t)f32_to_bf16_bits(hi) << 16);
+}
+
+// Eight e4m3fn bytes (two little-endian dwords, byte 0 = lowest K) decoded to
+// eight bf16 MFMA operand values: bf16(f32(e4m3(b)) * scale).
+__device__ __forceinline__ bf16x8 decode_fp8x8(uint32_t lo, uint32_t hi, float scale) {
+  const f32x2 a = __builtin_amdgcn_cvt_pk_f32_fp8(lo, false);
+  const f32x2 b = __builtin_amdgcn_cvt_pk_f32_fp8(lo, true);
+  const f32x2 c = __builtin_amdgcn_cvt_pk_f32_fp8(hi, false);
+  const f32x2 d = __builtin_amdgcn_cvt_pk_f32_fp8(hi, true);
+  bf16x8 r;
+  r[0] = (__bf16)(a[0] * scale);
+  r[1] = (__bf16)(a[1] * scale);
+  r[2] = (__bf16)(b[0] * scale);
+  r[3] = (__bf16)(b[1] * scale);
+  r[4] = (__bf16)(c[0] * scale);
+  r[5] = (__bf16)(c[1] * scale);
+  r[6] = (__bf16)(d[0] * scale);
+  r[7] = (__bf16)(d[1] * scale);
+  return r;
+}
+
+// Eight bf16 values held as four dwords reinterpreted as an MFMA operand.
+__device__ __forceinline__ bf16x8 as_bf16x8(u32x4 v) {
+  return __builtin_bit_cast(bf16x8, v);
+}
+
+// FP32 logistic 1 / (1 + exp(-x)).
+__device__ __forceinline__ float sigmoid_f32(float x) {
+  return 1.0f / (1.0f + expf(-x));
+}
+
+// bf16(bf16(g * bf16(sigmoid(g))) * u) with g, u already bf16 values: the
+// SwiGLU of the reference with one bf16 rounding per elementwise op
+// (glm_tpu/layers/moe/routed_experts.py:102,280).
+__device__ __forceinline__ float swiglu_bf16(float g, float u) {
+  const float s = round_to_bf16(sigmoid_f32(g));
+  return round_to_bf16(round_to_bf16(g * s) * u);
+}
+
+}  // namespace glm_moe

@@ -1,0 +1,127 @@
+// Internal launch interface between the C-ABI layer (capi.hip) and the kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace glm_moe {
+
+// ------------------------------------------------------------------ route plan
+constexpr int kPlanThreads = 1024;
+constexpr int kPlanWaves = kPlanThreads / 64;
+constexpr int kMaxExperts = 1024;
+
+struct RoutePlanArgs {
+  const int32_t* ids;        // [tokens * top_k] route expert ids (flat t * k + slot)
+  int32_t n;                 // tokens * top_k
+  int32_t top_k;
+  int32_t experts;
+  int32_t key_bits;          // bits needed to hold experts - 1 (wave match keys)
+  const float* route_w;      // nullable: also require finite, non-negative weights
+  int32_t* sorted;           // [n] sorted_flat_ids
+  int32_t* inverse;          // [n] inverse permutation (nullable)
+  int32_t* counts;           // [experts] group sizes
+  int32_t* offsets;          // [experts + 1] exclusive prefix of counts (nullable)
+  uint8_t* valid;            // [1]
+  // optional GEMM work list: one tile per tile_rows sorted routes of an expert
+  int32_t tile_rows;         // 0: no tiles
+  int32_t max_tiles;
+  int32_t* tile_expert;
+  int32_t* tile_row;
+  int32_t* tile_live;
+  int32_t* tile_count;       // [1]
+};
+hipError_t launch_route_plan(const RoutePlanArgs& a, hipStream_t stream);
+
+struct PanelPlanArgs {
+  const int32_t* group_sizes;  // [groups]
+  int32_t groups;
+  const int32_t* group_offset; // device scalar
+  int32_t rows;
+  int32_t local_groups;
+  int32_t panel_rows;
+  int32_t capacity;
+  int32_t* expert_ids;       // [capacity]
+  int32_t* row_starts;       // [capacity]
+  int32_t* live_counts;      // [capacity]
+  int32_t* active_panels;    // [1]
+  int32_t* restore_indices;  // [rows]
+  uint8_t* owned_rows;       // [rows]
+  uint8_t* valid;            // [1]
+};
+hipError_t launch_panel_plan(const PanelPlanArgs& a, hipStream_t stream);
+
+// Owned decode slots as one-row tiles (kernel.py:185-191 slot compaction).
+hipError_t launch_slot_tiles(const int32_t* local_ids, const uint8_t* owned, int32_t slots,
+                             int32_t experts, int32_t* tile_expert, int32_t* tile_row,
+                             int32_t* tile_live, int32_t* tile_count, hipStream_t stream);
+
+// ------------------------------------------------------------------ grouped FP8 GEMM
+enum Epilogue : int {
+  kEpiStoreF32 = 0,   // out[row][t*table_stride + n] = acc (f32)
+  kEpiStoreBf16 = 1,  // same, rounded to bf16
+  kEpiSwiglu = 2,     // out[row][n] = bf16 SwiGLU(bf16(gate), bf16(up))
+  kEpiWeighted = 3,   // out[row][n] = bf16(bf16(acc) * bf16(route_w[row]))
+};
+
+struct GroupedGemmArgs {
+  int32_t experts;             // tiles naming another expert are skipped
+  int32_t rows;                // sorted positions; tiles must lie in [0, rows)
+  int64_t x_rows;              // activation rows (gathered row ids are clamped to it)
+  int64_t out_rows;            // output rows (larger output row ids are skipped)
+  const uint16_t* x;           // bf16 activation rows of length k
+  const int32_t* x_row_ids;    // nullable: activation row of sorted position r = x_row_ids[r] / x_row_div
+  int32_t x_row_div;
+  const uint8_t* w0;           // [experts, n, k] e4m3fn bits
+  const float* s0;             // [experts, n/128, k/128]
+  const uint8_t* w1;           // second table (fused gate/up) or null
+  const float* s1;
+  int32_t n;
+  int32_t k;
+  const int32_t* tile_expert;  // work list
+  const int32_t* tile_row;
+  const int32_t* tile_live;
+  const int32_t* tile_count;
+  int32_t max_tiles;
+  const uint8_t* valid;        // nullable: no work at all when *valid == 0
+  void* out;
+  int64_t ldo;                 // elements between output rows
+  int64_t table_stride;        // elements between the tables of one output row
+  const int32_t* out_row_ids;  // nullable: output row of sorted position r
+  const float* route_w;        // kEpiWeighted: weight of output row
+};
+
+// Kernel shape families chosen by the host from the number of routes per tile.
+enum GemmShape : int {
+  kShapeSkinny = 0,  // <= 16 routes per tile, split-K over 4 waves (decode)
+  kShapePanel32 = 1, // <= 32 routes per tile (reference M32 panels)
+  kShapeWide = 2,    // <= 64 routes per tile (prefill)
+};
+int gemm_shape_rows(int shape);
+int gemm_shape_bn(int shape, int tables);
+hipError_t launch_grouped_gemm(const GroupedGemmArgs& a, int shape, int tables, int epilogue,
+                               hipStream_t stream);
+
+// ------------------------------------------------------------------ auxiliary
+hipError_t launch_decode_fp8_table(const uint8_t* bits, const float* scale, int64_t n, int64_t k,
+                                   int32_t block_n, int32_t block_k, uint16_t* out,
+                                   hipStream_t stream);
+hipError_t launch_gather_rows(const void* src, int64_t src_rows, int64_t row_bytes,
+                              const int32_t* index, int32_t div, const uint8_t* mask, int64_t n,
+                              void* dst, hipStream_t stream);
+hipError_t launch_pack_panel_rows(const void* src, int64_t src_rows, int64_t row_bytes,
+                                  const int32_t* row_starts, const int32_t* live_counts,
+                                  int32_t capacity, int32_t panel_rows, void* dst,
+                                  hipStream_t stream);
+hipError_t launch_zero_rows(void* out, int64_t rows, int64_t row_bytes, const uint8_t* keep,
+                            const uint8_t* valid, hipStream_t stream);
+// out[t] = bf16(sum over slots of y[t * top_k + s]); with ids != nullptr a slot
+// whose raw id is outside [0, experts) contributes nothing (decode ownership).
+hipError_t launch_combine_routes(const uint16_t* y, int64_t tokens, int32_t top_k, int64_t h,
+                                 const int32_t* ids, int32_t experts, int32_t bf16_sum,
+                                 uint16_t* out, hipStream_t stream);
+hipError_t launch_fill_u32(void* dst, int64_t words, uint32_t value, hipStream_t stream);
+hipError_t launch_synth_fp8(uint64_t seed, int32_t experts, int64_t n, int64_t k, float sigma,
+                            uint8_t* bits, float* scales, hipStream_t stream);
+
+}  // namespace glm_moe

@@ -1,0 +1,295 @@
+// Route planning: the stable expert grouping of glm-tpu's
+// group_prefill_routes (reference glm_tpu/layers/moe/routed_experts.py:139-164),
+// its expert-panel planner build_expert_panels
+// (glm_tpu/kernels/fp8_grouped_matmul/panels.py:26-83), and the GEMM work list.
+//
+// The grouping is a one-pass stable counting sort over the expert id:
+//   histogram (LDS integer counters: order-independent, so deterministic)
+//   -> exclusive scan over experts
+//   -> stable scatter: the rank of a route among equal ids before it comes from
+//      wave64 ballots (a 'match any' built from one ballot per key bit) plus a
+//      per-chunk scan of per-wave counts across the 16 waves, in wave order.
+// The result is bit-exact np.argsort(flat, kind="stable") / np.bincount.
+#include "moe_common.h"
+#include "moe_kernels.h"
+
+namespace glm_moe {
+
+namespace {
+
+// Exclusive scan of one int per thread over a 1024-thread block.
+// scratch holds kPlanWaves + 1 ints.  Returns the prefix; *total gets the sum.
+__device__ int block_exclusive_scan(int v, int* scratch, int* total) {
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  int x = v;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const int y = __shfl_up(x, d, 64);
+    if (lane >= d) x += y;
+  }
+  if (lane == 63) scratch[wave] = x;
+  __syncthreads();
+  if (wave == 0) {
+    const int t = lane < kPlanWaves ? scratch[lane] : 0;
+    int s = t;
+#pragma unroll
+    for (int d = 1; d < kPlanWaves; d <<= 1) {
+      const int y = __shfl_up(s, d, 64);
+      if (lane >= d) s += y;
+    }
+    if (lane < kPlanWaves) scratch[lane] = s - t;
+    if (lane == kPlanWaves - 1) scratch[kPlanWaves] = s;
+  }
+  __syncthreads();
+  const int r = x - v + scratch[wave];
+  *total = scratch[kPlanWaves];
+  __syncthreads();
+  return r;
+}
+
+__global__ __launch_bounds__(kPlanThreads) void route_plan_kernel(const RoutePlanArgs a) {
+  extern __shared__ int smem[];
+  const int E = a.experts;
+  const int ep = (E + 63) & ~63;
+  int* s_run = smem;                          // [ep] routes of each expert already placed
+  int* s_off = s_run + ep;                    // [ep] exclusive offsets
+  int* s_base = s_off + ep;                   // [ep] first position of an expert in this chunk
+  int* s_scan = s_base + ep;                  // [kPlanWaves + 1]
+  int* s_bad = s_scan + kPlanWaves + 1;       // [1]
+  uint16_t* s_pre = reinterpret_cast<uint16_t*>(s_bad + 1);            // [kPlanWaves][ep] wave prefix in chunk
+  uint8_t* s_wc = reinterpret_cast<uint8_t*>(s_pre + kPlanWaves * ep); // [kPlanWaves][ep] wave counts (<= 64)
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+
+  for (int i = tid; i < ep; i += kPlanThreads) s_run[i] = 0;
+  for (int i = tid; i < kPlanWaves * ep; i += kPlanThreads) s_wc[i] = 0;
+  for (int i = tid; i < kPlanWaves * ep; i += kPlanThreads) s_pre[i] = 0;
+  if (tid == 0) *s_bad = 0;
+  __syncthreads();
+
+  // histogram + range / weight validation
+  for (int i = tid; i < a.n; i += kPlanThreads) {
+    const int raw = a.ids[i];
+    const bool ok = raw >= 0 && raw < E;
+    if (!ok) atomicOr(s_bad, 1);
+    if (a.route_w) {
+      const float w = a.route_w[i];
+      if (!(w >= 0.0f) || isinf(w)) atomicOr(s_bad, 1);
+    }
+    atomicAdd(&s_run[ok ? raw : 0], 1);
+  }
+  // duplicate ids within one token's row (raw ids, as the reference compares them)
+  const int k = a.top_k;
+  const int tokens = a.n / k;
+  for (int t = tid; t < tokens; t += kPlanThreads) {
+    const int32_t* row = a.ids + (int64_t)t * k;
+    bool dup = false;
+    for (int i = 0; i < k && !dup; ++i) {
+      const int vi = row[i];
+      for (int j = i + 1; j < k; ++j) {
+        if (row[j] == vi) { dup = true; break; }
+      }
+    }
+    if (dup) atomicOr(s_bad, 1);
+  }
+  __syncthreads();
+
+  // counts and exclusive offsets (one expert per thread; experts <= 1024)
+  {
+    const int c = tid < E ? s_run[tid] : 0;
+    int total = 0;
+    const int ex = block_exclusive_scan(c, s_scan, &total);
+    if (tid < E) {
+      s_off[tid] = ex;
+      a.counts[tid] = c;
+      if (a.offsets) a.offsets[tid] = ex;
+      s_run[tid] = 0;
+    }
+    if (tid == 0 && a.offsets) a.offsets[E] = total;
+  }
+  __syncthreads();
+
+  // stable scatter, one 1024-route chunk at a time in route order
+  const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+  for (int base = 0; base < a.n; base += kPlanThreads) {
+    const int i = base + tid;
+    const bool act = i < a.n;
+    int e = 0;
+    if (act) {
+      const int raw = a.ids[i];
+      e = (raw >= 0 && raw < E) ? raw : 0;
+    }
+    uint64_t peers = __ballot(act);
+    for (int b = 0; b < a.key_bits; ++b) {
+      const bool bit = (e >> b) & 1;
+      const uint64_t m = __ballot(bit);
+      peers &= bit ? m : ~m;
+    }
+    const uint64_t before = peers & lt_mask;
+    const int rank = __popcll(before);
+    if (act && before == 0) s_wc[wave * ep + e] = (uint8_t)__popcll(peers);
+    __syncthreads();
+    // per expert: prefix over waves (in wave order), then advance the running count
+    for (int x = tid; x < E; x += kPlanThreads) {
+      int acc = 0;
+      for (int w = 0; w < kPlanWaves; ++w) {
+        const int c = s_wc[w * ep + x];
+        s_pre[w * ep + x] = (uint16_t)acc;
+        s_wc[w * ep + x] = 0;
+        acc += c;
+      }
+      s_base[x] = s_off[x] + s_run[x];
+      s_run[x] += acc;
+    }
+    __syncthreads();
+    if (act) {
+      const int pos = s_base[e] + s_pre[wave * ep + e] + rank;
+      if (pos >= 0 && pos < a.n) a.sorted[pos] = i;  // always true for a consistent plan
+      if (a.inverse) a.inverse[i] = pos;
+    }
+  }
+
+  const bool bad = *s_bad != 0;
+  if (tid == 0) a.valid[0] = bad ? 0 : 1;
+
+  // GEMM work list: ceil(count / tile_rows) tiles per expert, expert-major
+  if (a.tile_rows > 0) {
+    const int c = tid < E ? a.counts[tid] : 0;  // written above by this thread
+    const int nt = (c + a.tile_rows - 1) / a.tile_rows;
+    int total = 0;
+    const int t0 = block_exclusive_scan(nt, s_scan, &total);
+    if (tid < E) {
+      const int start = s_off[tid];
+      for (int j = 0; j < nt; ++j) {
+        const int idx = t0 + j;
+        if (idx < a.max_tiles) {
+          a.tile_expert[idx] = tid;
+          a.tile_row[idx] = start + j * a.tile_rows;
+          a.tile_live[idx] = min(a.tile_rows, c - j * a.tile_rows);
+        }
+      }
+    }
+    // An invalid route set is still planned with its safe ids (invalid -> 0),
+    // as the reference computes it; only the health byte reports it.
+    if (tid == 0) a.tile_count[0] = min(total, a.max_tiles);
+  }
+}
+
+// build_expert_panels (panels.py:26-83) for groups <= 1024 on one block.
+__global__ __launch_bounds__(kPlanThreads) void panel_plan_kernel(const PanelPlanArgs a) {
+  __shared__ int64_t s_ends[kMaxExperts];        // inclusive prefix of masked counts
+  __shared__ int64_t s_panel_ends[kMaxExperts];  // inclusive prefix of local panel counts
+  __shared__ int s_scan[kPlanWaves + 1];
+  __shared__ int s_bad;
+  __shared__ long long s_sum;
+  const int tid = threadIdx.x;
+  const int G = a.groups, L = a.local_groups, PR = a.panel_rows;
+  if (tid == 0) { s_bad = 0; s_sum = 0; }
+  __syncthreads();
+  const int size = tid < G ? a.group_sizes[tid] : 0;
+  if (tid < G && (size < 0 || size > a.rows)) atomicOr(&s_bad, 1);
+  if (tid < G) atomicAdd((unsigned long long*)&s_sum, (unsigned long long)(long long)size);
+  __syncthreads();
+  const int offset_raw = a.group_offset[0];
+  const bool valid = s_bad == 0 && s_sum == (long long)a.rows && offset_raw >= 0 &&
+                     offset_raw <= G - L;
+  const int offset = min(max(offset_raw, 0), G - L);
+  // ends = cumsum(where(valid, sizes, 0)); counts are in [0, rows] when valid
+  int total = 0;
+  const int c = valid ? size : 0;
+  const int ex = block_exclusive_scan(c, s_scan, &total);
+  if (tid < G) s_ends[tid] = (int64_t)ex + c;
+  __syncthreads();
+  // local panel counts and their inclusive prefix
+  const int lc = tid < L ? (int)(s_ends[offset + tid] - (offset + tid > 0 ? s_ends[offset + tid - 1] : 0)) : 0;
+  const int pc = (lc + PR - 1) / PR;
+  int ptotal = 0;
+  const int pex = block_exclusive_scan(pc, s_scan, &ptotal);
+  if (tid < L) s_panel_ends[tid] = (int64_t)pex + pc;
+  __syncthreads();
+  const int64_t last_panel_end = s_panel_ends[L - 1];
+  auto start_of = [&](int g) -> int64_t { return g > 0 ? s_ends[g - 1] : 0; };
+  auto panel_start_of = [&](int j) -> int64_t { return j > 0 ? s_panel_ends[j - 1] : 0; };
+  for (int p = tid; p < a.capacity; p += kPlanThreads) {
+    // searchsorted(panel_ends, p, side="right"): number of local groups with end <= p
+    int lo = 0, hi = L;
+    while (lo < hi) {
+      const int mid = (lo + hi) >> 1;
+      if (s_panel_ends[mid] <= p) lo = mid + 1; else hi = mid;
+    }
+    const int expert = min(lo, L - 1);
+    const int64_t within = ((int64_t)p - panel_start_of(expert)) * PR;
+    const bool active = p < last_panel_end;
+    const int64_t lcount = s_ends[offset + expert] - start_of(offset + expert);
+    a.expert_ids[p] = active ? expert : 0;
+    a.row_starts[p] = active ? (int32_t)(start_of(offset + expert) + within) : 0;
+    int64_t live = lcount - within;
+    live = live < 0 ? 0 : (live > PR ? PR : live);
+    a.live_counts[p] = active ? (int32_t)live : 0;
+  }
+  for (int r = tid; r < a.rows; r += kPlanThreads) {
+    int lo = 0, hi = G;
+    while (lo < hi) {
+      const int mid = (lo + hi) >> 1;
+      if (s_ends[mid] <= r) lo = mid + 1; else hi = mid;
+    }
+    const int re = min(lo, G - 1);
+    const bool owned = valid && re >= offset && re < offset + L;
+    const int lre = min(max(re - offset, 0), L - 1);
+    const int64_t rel = (int64_t)r - start_of(re);
+    const int64_t restore = panel_start_of(lre) * PR + rel;
+    a.restore_indices[r] = owned ? (int32_t)restore : 0;
+    a.owned_rows[r] = owned ? 1 : 0;
+  }
+  if (tid == 0) {
+    a.active_panels[0] = (int32_t)last_panel_end;
+    a.valid[0] = valid ? 1 : 0;
+  }
+}
+
+// Owned slots first, in slot order, as one-row tiles; ids clipped to [0, E).
+__global__ void slot_tiles_kernel(const int32_t* ids, const uint8_t* owned, int slots, int experts,
+                                  int32_t* tile_expert, int32_t* tile_row, int32_t* tile_live,
+                                  int32_t* tile_count) {
+  if (threadIdx.x != 0) return;
+  int n = 0;
+  for (int s = 0; s < slots; ++s) {
+    if (!owned[s]) continue;
+    const int e = min(max(ids[s], 0), experts - 1);
+    tile_expert[n] = e;
+    tile_row[n] = s;
+    tile_live[n] = 1;
+    ++n;
+  }
+  tile_count[0] = n;
+}
+
+}  // namespace
+
+hipError_t launch_route_plan(const RoutePlanArgs& a, hipStream_t stream) {
+  const int ep = (a.experts + 63) & ~63;
+  // int32 run/off/base + scan + flag, uint16 wave prefixes, uint8 wave counts:
+  // 60 KB at 1024 experts, 15 KB at 256.
+  const size_t lds = sizeof(int) * (size_t)(3 * ep + kPlanWaves + 2) +
+                     sizeof(uint16_t) * (size_t)kPlanWaves * ep + (size_t)kPlanWaves * ep;
+  hipLaunchKernelGGL(route_plan_kernel, dim3(1), dim3(kPlanThreads), lds, stream, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_panel_plan(const PanelPlanArgs& a, hipStream_t stream) {
+  hipLaunchKernelGGL(panel_plan_kernel, dim3(1), dim3(kPlanThreads), 0, stream, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_slot_tiles(const int32_t* local_ids, const uint8_t* owned, int32_t slots,
+                             int32_t experts, int32_t* tile_expert, int32_t* tile_row,
+                             int32_t* tile_live, int32_t* tile_count, hipStream_t stream) {
+  hipLaunchKernelGGL(slot_tiles_kernel, dim3(1), dim3(64), 0, stream, local_ids, owned, slots,
+                     experts, tile_expert, tile_row, tile_live, tile_count);
+  return hipGetLastError();
+}
+
+}  // namespace glm_moe

@@ -1,0 +1,146 @@
+"""ctypes binding of libglm_moe.so (the C ABI declared in include/glm_moe.h).
+
+The library is built in-tree by ``glm-tpu_amd/build.py``.  There is no
+fallback: if the library is missing every entry point raises, and tensors must
+already live on the GPU.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+LIB_PATH = Path(__file__).resolve().with_name("libglm_moe.so")
+HEADER_PATH = Path(__file__).resolve().parents[2] / "include" / "glm_moe.h"
+
+OK = 0
+ERR_ARGUMENT = 1
+ERR_WORKSPACE = 2
+ERR_DEVICE = 3
+
+F32 = 0
+BF16 = 1
+
+ROUTE_SUM_BF16 = 0x1
+CHECK_WEIGHTS = 0x2
+DROP_UNOWNED = 0x4
+
+_vp = ctypes.c_void_p
+_i32 = ctypes.c_int32
+_i64 = ctypes.c_int64
+_u32 = ctypes.c_uint32
+_sz = ctypes.c_size_t
+_f = ctypes.c_float
+
+# name -> (restype, argtypes); kept in the order of include/glm_moe.h
+SIGNATURES: dict[str, tuple] = {
+    "glm_moe_abi_version": (ctypes.c_int, []),
+    "glm_moe_last_error": (ctypes.c_char_p, []),
+    "glm_moe_decode_fp8_table": (ctypes.c_int, [_vp, _vp, _i64, _i64, _i32, _i32, _vp, _vp]),
+    "glm_moe_group_routes": (ctypes.c_int, [_vp, _i64, _i32, _i32, _vp, _vp, _vp, _vp, _vp]),
+    "glm_moe_gather_rows": (ctypes.c_int, [_vp, _i64, _i64, _vp, _i32, _vp, _i64, _vp, _vp]),
+    "glm_moe_build_expert_panels": (
+        ctypes.c_int,
+        [_vp, _i32, _vp, _i32, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp],
+    ),
+    "glm_moe_pack_expert_panel_rows": (ctypes.c_int, [_vp, _i64, _i64, _vp, _vp, _i32, _vp, _vp]),
+    "glm_moe_panel_fp8_matmul": (
+        ctypes.c_int,
+        [_vp, _i64, _i64, _vp, _vp, _i32, _i64, _vp, _vp, _vp, _vp, _i32, _vp, _vp, _i32, _vp, _vp],
+    ),
+    "glm_moe_routed_projection_workspace_bytes": (_sz, [_i32]),
+    "glm_moe_routed_projection": (
+        ctypes.c_int,
+        [_vp, _i32, _i64, _i32, _vp, _vp, _vp, _vp, _i32, _i64, _vp, _vp, _i32, _vp, _vp, _sz, _vp],
+    ),
+    "glm_moe_routed_experts_workspace_bytes": (_sz, [_i64, _i32, _i32, _i64, _i64]),
+    "glm_moe_routed_experts": (
+        ctypes.c_int,
+        [_vp, _i64, _i64, _vp, _vp, _i32, _i32, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _u32, _vp, _vp, _vp, _sz, _vp],
+    ),
+    "glm_moe_event_create": (ctypes.c_int, [ctypes.POINTER(_vp)]),
+    "glm_moe_event_destroy": (ctypes.c_int, [_vp]),
+    "glm_moe_event_elapsed_ms": (ctypes.c_int, [_vp, _vp, ctypes.POINTER(_f)]),
+    "glm_moe_routed_experts_timed": (
+        ctypes.c_int,
+        [_vp, _i64, _i64, _vp, _vp, _i32, _i32, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _u32, _vp, _vp, _vp, _sz, _vp, _vp],
+    ),
+    "glm_moe_synthesize_fp8_weights": (ctypes.c_int, [ctypes.c_uint64, _i32, _i64, _i64, _f, _vp, _vp, _vp]),
+}
+
+_LIB: ctypes.CDLL | None = None
+
+
+class GlmMoeDeviceError(RuntimeError):
+    """A HIP runtime error reported by libglm_moe.so."""
+
+
+def header_functions() -> list[str]:
+    """Names of every function declared in include/glm_moe.h."""
+    text = HEADER_PATH.read_text()
+    return re.findall(r"^\s*(?:int|size_t|const char\*)\s+(glm_moe_\w+)\s*\(", text, flags=re.M)
+
+
+def lib() -> ctypes.CDLL:
+    """Load the library once; raise if it was not built."""
+    global _LIB
+    if _LIB is None:
+        if not LIB_PATH.exists():
+            raise RuntimeError(
+                f"{LIB_PATH} is missing: build it with `python glm-tpu_amd/build.py` "
+                "(the MoE path has no CPU fallback)"
+            )
+        handle = ctypes.CDLL(str(LIB_PATH))
+        for name, (restype, argtypes) in SIGNATURES.items():
+            fn = getattr(handle, name)
+            fn.restype = restype
+            fn.argtypes = argtypes
+        if handle.glm_moe_abi_version() != 1:
+            raise RuntimeError("libglm_moe.so ABI version mismatch")
+        _LIB = handle
+    return _LIB
+
+
+def check(status: int) -> None:
+    """Map a glm_moe_status to the reference's exception types."""
+    if status == OK:
+        return
+    message = (lib().glm_moe_last_error() or b"").decode(errors="replace")
+    if status in (ERR_ARGUMENT, ERR_WORKSPACE):
+        raise ValueError(message)
+    raise GlmMoeDeviceError(message)
+
+
+def call(name: str, *args) -> None:
+    check(getattr(lib(), name)(*args))
+
+
+def ptr(tensor) -> ctypes.c_void_p:
+    """Device pointer of a tensor (None -> NULL)."""
+    if tensor is None:
+        return ctypes.c_void_p(0)
+    return ctypes.c_void_p(tensor.data_ptr())
+
+
+def stream_of(tensor) -> ctypes.c_void_p:
+    """The current torch stream of the tensor's device as a hipStream_t."""
+    import torch
+
+    return ctypes.c_void_p(torch.cuda.current_stream(tensor.device).cuda_stream)
+
+
+def require_device(*tensors) -> None:
+    """Every tensor must be on the same GPU (there is no CPU path)."""
+    device = None
+    for t in tensors:
+        if t is None:
+            continue
+        if not t.is_cuda:
+            raise ValueError("glm_moe kernels take GPU tensors only (no CPU fallback)")
+        if device is None:
+            device = t.device
+        elif t.device != device:
+            raise ValueError("glm_moe tensors must share one device")
+        if not t.is_contiguous():
+            raise ValueError("glm_moe tensors must be contiguous")

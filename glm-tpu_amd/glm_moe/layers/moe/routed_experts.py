@@ -1,0 +1,363 @@
+"""The routed-expert MoE layer bodies on one MI355X, backed by libglm_moe.
+
+Mirrors ``glm_tpu/layers/moe/routed_experts.py`` of the reference with the same
+names, parameter lists and arithmetic boundaries:
+
+* ``prefill_moe_from_routes`` (``:27-128``): rows ``[T, H]`` -> (bf16 output, health);
+* ``moe_grouped_routes`` (``:186-304``): the one-row decode body;
+* ``PrefillRoutes`` / ``group_prefill_routes`` / ``gather_prefill_route_rows`` /
+  ``restore_prefill_route_rows`` (``:130-183``).
+
+The routed half runs as one HIP pipeline (``routed_experts`` below): a stable
+counting-sort route plan, the fused gate/up FP8 projection with bf16 SwiGLU,
+the down FP8 projection with bf16 route weighting, and the route combine.
+Work is launched only for the experts the routes select.  On one GPU every
+mesh axis has size 1: ``hidden_local`` is the full hidden state, every expert
+is local and both ``psum`` of the reference are the identity.
+
+The shared expert and ``routed * 2.5 + shared`` use torch bf16 GEMMs on the
+same GPU (hipBLASLt), at the reference's rounding points.
+"""
+
+from __future__ import annotations
+
+from typing import Any, NamedTuple
+
+import torch
+
+from glm_moe import _lib
+from glm_moe.contracts import GlmMoeNumericalContract, single_gpu_contract
+from glm_moe.kernels.fp8_grouped_matmul.kernel import RoutedProjectionConfig
+
+
+class PrefillRoutes(NamedTuple):
+    """Permutation metadata; ``valid`` MUST join the caller's serving health."""
+
+    sorted_flat_ids: torch.Tensor
+    inverse_permutation: torch.Tensor
+    group_sizes: torch.Tensor
+    valid: torch.Tensor
+
+
+def group_prefill_routes(route_indices: torch.Tensor, *, num_experts: int = 256) -> PrefillRoutes:
+    """Group by expert, preserving original token/slot order inside each group.
+
+    Invalid dynamic ids or duplicate experts produce ``valid=False``; they are
+    not silently admitted (``routed_experts.py:139-164``).
+    """
+    if route_indices.ndim != 2 or min(route_indices.shape) <= 0:
+        raise ValueError("routes must be nonempty [tokens,top_k]")
+    if route_indices.dtype != torch.int32:
+        raise ValueError("routes must be int32")
+    if not isinstance(num_experts, int) or isinstance(num_experts, bool) or num_experts <= 0:
+        raise ValueError("num_experts must be a positive integer")
+    if route_indices.shape[1] > num_experts:
+        raise ValueError("top_k exceeds expert count")
+    _lib.require_device(route_indices)
+    tokens, top_k = route_indices.shape
+    device = route_indices.device
+    n = tokens * top_k
+    order = torch.empty(n, dtype=torch.int32, device=device)
+    inverse = torch.empty(n, dtype=torch.int32, device=device)
+    counts = torch.empty(num_experts, dtype=torch.int32, device=device)
+    valid = torch.empty((), dtype=torch.bool, device=device)
+    _lib.call(
+        "glm_moe_group_routes",
+        _lib.ptr(route_indices), tokens, top_k, num_experts, _lib.ptr(order), _lib.ptr(inverse),
+        _lib.ptr(counts), _lib.ptr(valid), _lib.stream_of(route_indices),
+    )
+    return PrefillRoutes(order, inverse, counts, valid)
+
+
+def _gather(values: torch.Tensor, index: torch.Tensor, div: int, rows: int) -> torch.Tensor:
+    _lib.require_device(values, index)
+    flat = values.reshape(values.shape[0], -1)
+    row_bytes = flat.shape[1] * flat.element_size()
+    if row_bytes % 4:
+        raise ValueError("gathered rows must be a multiple of 4 bytes")
+    out = torch.empty((rows, *values.shape[1:]), dtype=values.dtype, device=values.device)
+    _lib.call("glm_moe_gather_rows", _lib.ptr(flat), flat.shape[0], row_bytes, _lib.ptr(index), div,
+              _lib.ptr(None), rows, _lib.ptr(out), _lib.stream_of(values))
+    return out
+
+
+def gather_prefill_route_rows(hidden: torch.Tensor, routes: PrefillRoutes, *, top_k: int) -> torch.Tensor:
+    """``hidden[sorted_flat_ids // top_k]`` (``routed_experts.py:167-171``)."""
+    if hidden.ndim != 2 or top_k <= 0 or tuple(routes.sorted_flat_ids.shape) != (hidden.shape[0] * top_k,):
+        raise ValueError("hidden and route geometry disagree")
+    return _gather(hidden, routes.sorted_flat_ids, top_k, routes.sorted_flat_ids.numel())
+
+
+def restore_prefill_route_rows(sorted_values: torch.Tensor, routes: PrefillRoutes, *, top_k: int) -> torch.Tensor:
+    """``sorted_values[inverse].reshape(T, top_k, F)`` (``routed_experts.py:174-183``)."""
+    if (
+        sorted_values.ndim != 2
+        or top_k <= 0
+        or sorted_values.shape[0] != routes.inverse_permutation.numel()
+        or sorted_values.shape[0] % top_k
+    ):
+        raise ValueError("sorted output and route geometry disagree")
+    restored = _gather(sorted_values, routes.inverse_permutation, 1, sorted_values.shape[0])
+    return restored.reshape(-1, top_k, sorted_values.shape[-1])
+
+
+class RoutedTimings(NamedTuple):
+    """Stage times (ms) of one ``routed_experts`` call, measured with HIP events."""
+
+    plan: float
+    gate_up: float
+    down: float
+    combine: float
+
+    @property
+    def total(self) -> float:
+        return self.plan + self.gate_up + self.down + self.combine
+
+
+class StageEvents:
+    """Five HIP events recorded around the stages of ``routed_experts``."""
+
+    def __init__(self) -> None:
+        import ctypes
+
+        self._handles = []
+        for _ in range(5):
+            slot = ctypes.c_void_p()
+            _lib.call("glm_moe_event_create", ctypes.byref(slot))
+            self._handles.append(slot.value)
+        self.array = (ctypes.c_void_p * 5)(*self._handles)
+
+    def elapsed(self) -> RoutedTimings:
+        import ctypes
+
+        ms = []
+        for i in range(4):
+            value = ctypes.c_float()
+            _lib.call("glm_moe_event_elapsed_ms", ctypes.c_void_p(self._handles[i]),
+                      ctypes.c_void_p(self._handles[i + 1]), ctypes.byref(value))
+            ms.append(value.value)
+        return RoutedTimings(*ms)
+
+    def close(self) -> None:
+        import ctypes
+
+        for handle in self._handles:
+            _lib.call("glm_moe_event_destroy", ctypes.c_void_p(handle))
+        self._handles = []
+
+
+_WORKSPACES: dict[tuple, torch.Tensor] = {}
+
+
+def routed_workspace(tokens: int, top_k: int, num_experts: int, hidden: int, intermediate: int,
+                     device: torch.device) -> torch.Tensor:
+    """The caller-owned workspace of ``routed_experts`` (cached per shape and device)."""
+    key = (tokens, top_k, num_experts, hidden, intermediate, str(device))
+    ws = _WORKSPACES.get(key)
+    if ws is None:
+        nbytes = _lib.lib().glm_moe_routed_experts_workspace_bytes(tokens, top_k, num_experts, hidden, intermediate)
+        ws = torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=device)
+        _WORKSPACES[key] = ws
+    return ws
+
+
+def routed_experts(
+    hidden: torch.Tensor,
+    route_indices: torch.Tensor,
+    route_weights: torch.Tensor,
+    gate_bits: torch.Tensor,
+    gate_scale: torch.Tensor,
+    up_bits: torch.Tensor,
+    up_scale: torch.Tensor,
+    down_bits: torch.Tensor,
+    down_scale: torch.Tensor,
+    *,
+    route_sum: str = "float32",
+    check_weights: bool = True,
+    drop_unowned: bool = False,
+    out: torch.Tensor | None = None,
+    events: StageEvents | None = None,
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """Routed experts of ``[T, H]`` bf16 rows: ``(bf16 [T, H], valid)``.
+
+    The routed half of ``prefill_moe_from_routes`` (``routed_experts.py:82-117``):
+    FP32 gate/up projections, bf16 SwiGLU, bf16 down projection, bf16 route
+    weighting and the sum over the top-k slots (``route_sum``: FP32 with one
+    rounding, or ``"bfloat16"`` for the decode body's bf16 sum, ``:293``).
+    """
+    if hidden.ndim != 2 or hidden.dtype != torch.bfloat16:
+        raise ValueError("routed experts take bf16 [tokens, hidden] rows")
+    tokens, h = hidden.shape
+    if route_indices.ndim != 2 or route_indices.shape[0] != tokens or route_indices.dtype != torch.int32:
+        raise ValueError("route indices must be int32 [tokens, top_k]")
+    top_k = route_indices.shape[1]
+    if tuple(route_weights.shape) != (tokens, top_k) or route_weights.dtype != torch.float32:
+        raise ValueError("route weights must be float32 [tokens, top_k]")
+    if gate_bits.ndim != 3 or gate_bits.dtype != torch.uint8:
+        raise ValueError("expert gate bits must be uint8 [E, I, H]")
+    experts, inter, gh = gate_bits.shape
+    if gh != h or tuple(up_bits.shape) != (experts, inter, h) or tuple(down_bits.shape) != (experts, h, inter):
+        raise ValueError("expert table geometry disagrees with the hidden size")
+    if up_bits.dtype != torch.uint8 or down_bits.dtype != torch.uint8:
+        raise ValueError("expert tables must be uint8 e4m3fn bits")
+    for scale, rows, cols in ((gate_scale, inter, h), (up_scale, inter, h), (down_scale, h, inter)):
+        if scale.dtype != torch.float32 or tuple(scale.shape) != (experts, rows // 128, cols // 128):
+            raise ValueError("expert scales must be float32 [E, N/128, K/128]")
+    if route_sum not in ("float32", "bfloat16"):
+        raise ValueError("route_sum must be float32 or bfloat16")
+    _lib.require_device(hidden, route_indices, route_weights, gate_bits, gate_scale, up_bits, up_scale,
+                        down_bits, down_scale, out)
+    device = hidden.device
+    if out is None:
+        out = torch.empty((tokens, h), dtype=torch.bfloat16, device=device)
+    elif tuple(out.shape) != (tokens, h) or out.dtype != torch.bfloat16:
+        raise ValueError("out must be bf16 [tokens, hidden]")
+    valid = torch.empty((), dtype=torch.bool, device=device)
+    ws = routed_workspace(tokens, top_k, experts, h, inter, device)
+    flags = 0
+    if route_sum == "bfloat16":
+        flags |= _lib.ROUTE_SUM_BF16
+    if check_weights:
+        flags |= _lib.CHECK_WEIGHTS
+    if drop_unowned:
+        flags |= _lib.DROP_UNOWNED
+    args = [
+        _lib.ptr(hidden), tokens, h, _lib.ptr(route_indices), _lib.ptr(route_weights), top_k, experts, inter,
+        _lib.ptr(gate_bits), _lib.ptr(gate_scale), _lib.ptr(up_bits), _lib.ptr(up_scale), _lib.ptr(down_bits),
+        _lib.ptr(down_scale), flags, _lib.ptr(out), _lib.ptr(valid), _lib.ptr(ws), ws.numel(),
+    ]
+    if events is None:
+        _lib.call("glm_moe_routed_experts", *args, _lib.stream_of(hidden))
+    else:
+        _lib.call("glm_moe_routed_experts_timed", *args, events.array, _lib.stream_of(hidden))
+    return out, valid
+
+
+def _shared_swiglu(hidden: torch.Tensor, gate: torch.Tensor, up: torch.Tensor, down: torch.Tensor) -> torch.Tensor:
+    """The bf16-resident shared expert at the reference's rounding points.
+
+    FP32-accumulated gate/up rounded to bf16 (``routed_experts.py:119-122`` /
+    ``:269-279``), bf16 SwiGLU one op at a time (``:123`` / ``:280``), bf16 down
+    projection with FP32 accumulation and one rounding (``:124`` / ``:297-302``).
+    """
+    g = hidden @ gate.t()
+    u = hidden @ up.t()
+    act = (g * torch.sigmoid(g)) * u
+    return act @ down.t()
+
+
+def _check_layer_shapes(hidden_local, route_indices, route_weights, gate_bits, up_bits, down_bits,
+                        contract: GlmMoeNumericalContract, *, rows_exact: int | None) -> None:
+    if contract.stage_size != 1:
+        raise ValueError("one-GPU MoE holds every expert: contract.stage_size must be 1")
+    if hidden_local.ndim != 2 or hidden_local.shape[0] <= 0 or hidden_local.dtype != torch.bfloat16:
+        raise ValueError("MoE requires BF16 live rows")
+    if rows_exact is not None and hidden_local.shape[0] != rows_exact:
+        raise ValueError("grouped MoE input must contain one live row")
+    if hidden_local.shape[1] != contract.hidden_size:
+        raise ValueError("MoE hidden size differs from contract")
+    expected = (hidden_local.shape[0], contract.top_k)
+    if tuple(route_indices.shape) != expected or tuple(route_weights.shape) != expected:
+        raise ValueError("routing geometry differs from contract")
+    if route_indices.dtype != torch.int32:
+        raise ValueError("routes must be int32")
+    if route_weights.dtype != torch.float32:
+        raise ValueError("route weights must be FP32")
+    gate_shape = (contract.local_experts, contract.intermediate_size, contract.hidden_size)
+    if tuple(gate_bits.shape) != gate_shape or tuple(up_bits.shape) != gate_shape:
+        raise ValueError("expert gate/up geometry differs from contract")
+    if tuple(down_bits.shape) != (contract.local_experts, contract.hidden_size, contract.intermediate_size):
+        raise ValueError("expert down geometry differs from contract")
+
+
+def prefill_moe_from_routes(
+    hidden_local: torch.Tensor,
+    route_indices: torch.Tensor,
+    route_weights: torch.Tensor,
+    expert_gate_bits_local: torch.Tensor,
+    expert_gate_scale_local: torch.Tensor,
+    expert_up_bits_local: torch.Tensor,
+    expert_up_scale_local: torch.Tensor,
+    expert_down_bits_local: torch.Tensor,
+    expert_down_scale_local: torch.Tensor,
+    shared_gate_local: torch.Tensor,
+    shared_up_local: torch.Tensor,
+    shared_down_local: torch.Tensor,
+    *,
+    contract: GlmMoeNumericalContract = single_gpu_contract(),
+    interpret: bool = False,
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """Return (hidden ``[T, H]`` bf16, health) of one prefill MoE layer.
+
+    ``routed_experts.py:27-128``.  A false health bit forbids serving; it must
+    not be discarded by a caller.
+    """
+    del interpret
+    _check_layer_shapes(hidden_local, route_indices, route_weights, expert_gate_bits_local,
+                        expert_up_bits_local, expert_down_bits_local, contract, rows_exact=None)
+    if contract.fp8_block_shape != (128, 128):
+        raise ValueError("expert panels require checkpoint scale blocks128x128")
+    inter, h = contract.intermediate_size, contract.hidden_size
+    if (
+        tuple(shared_gate_local.shape) != (inter, h)
+        or tuple(shared_up_local.shape) != (inter, h)
+        or tuple(shared_down_local.shape) != (h, inter)
+    ):
+        raise ValueError("prefill shared expert geometry differs from contract")
+    routed, valid = routed_experts(
+        hidden_local, route_indices, route_weights, expert_gate_bits_local, expert_gate_scale_local,
+        expert_up_bits_local, expert_up_scale_local, expert_down_bits_local, expert_down_scale_local,
+        route_sum="float32", check_weights=True,
+    )
+    shared = _shared_swiglu(hidden_local, shared_gate_local, shared_up_local, shared_down_local)
+    scale = torch.tensor(contract.routed_scaling_factor, dtype=torch.bfloat16, device=routed.device)
+    output = routed * scale + shared
+    valid = valid & torch.isfinite(output).all()
+    return output, valid
+
+
+def moe_grouped_routes(
+    hidden_local: torch.Tensor,
+    route_indices: torch.Tensor,
+    route_weights: torch.Tensor,
+    expert_gate_bits_local: torch.Tensor,
+    expert_gate_scale_local: torch.Tensor,
+    expert_up_bits_local: torch.Tensor,
+    expert_up_scale_local: torch.Tensor,
+    expert_down_bits_local: torch.Tensor,
+    expert_down_scale_local: torch.Tensor,
+    *,
+    contract: GlmMoeNumericalContract = single_gpu_contract(),
+    config: RoutedProjectionConfig = RoutedProjectionConfig(),
+    expert_axis: str = "expert",
+    feature_axis: str = "feature",
+    interpret: bool = False,
+    shared_bf16: tuple[Any, Any, Any],
+) -> torch.Tensor:
+    """The decode MoE of one row with route-grouped routed experts (``routed_experts.py:186-304``).
+
+    Routes whose id lies outside ``[0, E)`` are not owned and contribute zero
+    (``:250-253``); the weighted routes are summed in bf16 (``:293``).
+    """
+    del expert_axis, feature_axis, interpret
+    _check_layer_shapes(hidden_local, route_indices, route_weights, expert_gate_bits_local,
+                        expert_up_bits_local, expert_down_bits_local, contract, rows_exact=1)
+    if tuple(config.block_shape) != tuple(contract.fp8_block_shape):
+        raise ValueError("grouped MoE tile config block differs from the contract")
+    inter, h = contract.intermediate_size, contract.hidden_size
+    if (
+        len(shared_bf16) != 3
+        or any(t.dtype != torch.bfloat16 for t in shared_bf16)
+        or tuple(shared_bf16[0].shape) != (inter, h)
+        or tuple(shared_bf16[1].shape) != (inter, h)
+        or tuple(shared_bf16[2].shape) != (h, inter)
+    ):
+        raise ValueError("grouped MoE BF16 shared tables drifted")
+    routed, _ = routed_experts(
+        hidden_local, route_indices, route_weights, expert_gate_bits_local, expert_gate_scale_local,
+        expert_up_bits_local, expert_up_scale_local, expert_down_bits_local, expert_down_scale_local,
+        route_sum="bfloat16", check_weights=False, drop_unowned=True,
+    )
+    shared = _shared_swiglu(hidden_local, *shared_bf16)
+    scale = torch.tensor(contract.routed_scaling_factor, dtype=torch.bfloat16, device=routed.device)
+    return routed * scale + shared

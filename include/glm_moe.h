@@ -1,0 +1,168 @@
+/*
+ * glm_moe.h -- C ABI of the MI355X (gfx950) routed-expert MoE library
+ * (libglm_moe.so), the drop-in backend of glm-tpu's route-grouped FP8
+ * routed-expert path.
+ *
+ * Every entry point takes plain device pointers and sizes, never allocates,
+ * and enqueues its kernels on `stream` (a hipStream_t; NULL = default stream).
+ * Nothing synchronises with the host: dynamic validity is written to a device
+ * byte, exactly as the reference keeps its health bit on device.
+ *
+ * Return values: GLM_MOE_OK, or a status whose message glm_moe_last_error()
+ * returns (thread-local).  GLM_MOE_ERR_ARGUMENT is the static shape/dtype
+ * refusal the reference raises as ValueError at trace time.
+ *
+ * Tensor layouts (row-major, checkpoint [out, in] orientation):
+ *   hidden        bf16 [tokens, H]          (uint16_t bit patterns)
+ *   route ids     int32 [tokens, top_k], flat index t * top_k + slot
+ *   route weights f32 [tokens, top_k]
+ *   gate/up bits  uint8 e4m3fn [E, I, H],  scales f32 [E, I/128, H/128]
+ *   down bits     uint8 e4m3fn [E, H, I],  scales f32 [E, H/128, I/128]
+ *
+ * Each declaration names the reference interface (GianluigiVitale/glm-tpu,
+ * file:line) that it replaces.
+ */
+#ifndef GLM_MOE_H
+#define GLM_MOE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define GLM_MOE_ABI_VERSION 1
+
+enum glm_moe_status {
+  GLM_MOE_OK = 0,
+  GLM_MOE_ERR_ARGUMENT = 1,  /* static geometry / dtype refusal (ValueError) */
+  GLM_MOE_ERR_WORKSPACE = 2, /* workspace smaller than *_workspace_bytes() */
+  GLM_MOE_ERR_DEVICE = 3     /* HIP runtime error (launch or device) */
+};
+
+enum glm_moe_dtype { GLM_MOE_F32 = 0, GLM_MOE_BF16 = 1 };
+
+/* glm_moe_routed_experts flags */
+#define GLM_MOE_ROUTE_SUM_BF16 0x1u   /* bf16 running route sum (decode body, routed_experts.py:293) */
+#define GLM_MOE_CHECK_WEIGHTS 0x2u    /* weights must be finite and >= 0 (prefill health, routed_experts.py:83) */
+#define GLM_MOE_DROP_UNOWNED 0x4u     /* routes with ids outside [0, E) contribute zero (decode ownership, routed_experts.py:250-253) */
+
+int glm_moe_abi_version(void);
+const char* glm_moe_last_error(void);
+
+/* Replaces glm_tpu/layers/fp8.py:113-126 decode_fp8_table (and the
+ * dequantize_fp8_bits_block_weight arithmetic, :37-72):
+ * out[n][k] = bf16(f32(e4m3(bits[n][k])) * scale[n / block_n][k / block_k]),
+ * scale is [ceil(n / block_n), ceil(k / block_k)]. */
+int glm_moe_decode_fp8_table(const uint8_t* bits, const float* scale, int64_t n, int64_t k,
+                             int32_t block_n, int32_t block_k, uint16_t* out_bf16, void* stream);
+
+/* Replaces glm_tpu/layers/moe/routed_experts.py:139-164 group_prefill_routes:
+ * sorted_flat_ids = argsort(flat ids, stable), inverse_permutation, group_sizes
+ * = bincount (invalid ids count as expert 0), *valid = all ids in [0, E) and no
+ * duplicate id within a token's row.  num_experts <= 1024. */
+int glm_moe_group_routes(const int32_t* route_indices, int64_t tokens, int32_t top_k,
+                         int32_t num_experts, int32_t* sorted_flat_ids,
+                         int32_t* inverse_permutation, int32_t* group_sizes, uint8_t* valid,
+                         void* stream);
+
+/* Replaces glm_tpu/layers/moe/routed_experts.py:167-183 gather_prefill_route_rows /
+ * restore_prefill_route_rows and panels.py:98-104 unpack_expert_panel_rows:
+ * dst[i] = mask[i] ? src[clamp(index[i], 0, src_rows - 1) / div] : 0, whole rows of
+ * row_bytes (a multiple of 4).  mask may be NULL (keep every row). */
+int glm_moe_gather_rows(const void* src, int64_t src_rows, int64_t row_bytes,
+                        const int32_t* index, int32_t div, const uint8_t* mask, int64_t rows,
+                        void* dst, void* stream);
+
+/* Replaces glm_tpu/kernels/fp8_grouped_matmul/panels.py:26-83 build_expert_panels
+ * (32-row panels; capacity = ceil(rows / 32) + local_groups - 1).  group_offset is
+ * a device int32 scalar.  num_groups <= 1024. */
+int glm_moe_build_expert_panels(const int32_t* group_sizes, int32_t num_groups,
+                                const int32_t* group_offset, int32_t rows, int32_t local_groups,
+                                int32_t* expert_ids, int32_t* row_starts, int32_t* live_counts,
+                                int32_t* active_panels, int32_t* restore_indices,
+                                uint8_t* owned_rows, uint8_t* valid, void* stream);
+
+/* Replaces panels.py:86-95 pack_expert_panel_rows: out [capacity, 32, row] with
+ * rows past a panel's live count zero. */
+int glm_moe_pack_expert_panel_rows(const void* values, int64_t rows, int64_t row_bytes,
+                                   const int32_t* row_starts, const int32_t* live_counts,
+                                   int32_t capacity, void* out, void* stream);
+
+/* Replaces glm_tpu/kernels/fp8_grouped_matmul/panel_kernel.py:31-153
+ * prefill_panel_fp8_matmul: sorted bf16 rows lhs [m, k] against their panel's local
+ * expert ([groups, n, k] bits, [groups, n/128, k/128] scales), FP32 accumulation,
+ * out [m, n] f32 or bf16 in sorted row order; unowned rows, and every row of an
+ * invalid plan, are zero.  The plan is build_expert_panels' output. */
+int glm_moe_panel_fp8_matmul(const uint16_t* lhs, int64_t m, int64_t k, const uint8_t* weight_bits,
+                             const float* scale, int32_t groups, int64_t n,
+                             const int32_t* panel_expert_ids, const int32_t* panel_row_starts,
+                             const int32_t* panel_live_counts, const int32_t* active_panels,
+                             int32_t capacity, const uint8_t* owned_rows, const uint8_t* valid,
+                             int32_t result_dtype, void* out, void* stream);
+
+/* Replaces glm_tpu/kernels/fp8_grouped_matmul/kernel.py:125-299 fp8_routed_projection:
+ * one bf16 row per route slot lhs [slots, k] against the slot's expert
+ * (ids clipped to [0, experts)) in 1 or 2 tables; out [slots, tables, n] f32 or bf16;
+ * unowned slots are zero.  Needs glm_moe_routed_projection_workspace_bytes(slots). */
+size_t glm_moe_routed_projection_workspace_bytes(int32_t slots);
+int glm_moe_routed_projection(const uint16_t* lhs, int32_t slots, int64_t k, int32_t tables,
+                              const uint8_t* bits0, const float* scale0, const uint8_t* bits1,
+                              const float* scale1, int32_t experts, int64_t n,
+                              const int32_t* local_expert_ids, const uint8_t* owned,
+                              int32_t result_dtype, void* out, void* workspace,
+                              size_t workspace_bytes, void* stream);
+
+/* The routed-expert half of glm_tpu/layers/moe/routed_experts.py:27-128
+ * prefill_moe_from_routes (and of :186-304 moe_grouped_routes) on one device:
+ * group routes -> gate/up FP8 projections with fused bf16 SwiGLU -> down FP8
+ * projection with fused bf16 route weighting -> FP32 route sum (one bf16
+ * rounding; GLM_MOE_ROUTE_SUM_BF16 for the decode body's bf16 sum).
+ * out bf16 [tokens, H]; *valid = all ids in [0, E), no duplicate id in a row (and
+ * weights finite >= 0 with GLM_MOE_CHECK_WEIGHTS).  As in the reference, an
+ * invalid route set is still computed with its safe ids (an out-of-range id
+ * counts as expert 0) and only *valid reports it; with GLM_MOE_DROP_UNOWNED an
+ * out-of-range route instead contributes zero (the decode body's ownership).
+ * Work is launched only for the experts the routes select. */
+size_t glm_moe_routed_experts_workspace_bytes(int64_t tokens, int32_t top_k, int32_t num_experts,
+                                              int64_t hidden, int64_t intermediate);
+int glm_moe_routed_experts(const uint16_t* hidden, int64_t tokens, int64_t hidden_size,
+                           const int32_t* route_indices, const float* route_weights,
+                           int32_t top_k, int32_t num_experts, int64_t intermediate,
+                           const uint8_t* gate_bits, const float* gate_scale,
+                           const uint8_t* up_bits, const float* up_scale,
+                           const uint8_t* down_bits, const float* down_scale, uint32_t flags,
+                           uint16_t* out, uint8_t* valid, void* workspace, size_t workspace_bytes,
+                           void* stream);
+
+/* Stage timing for benchmarks: glm_moe_routed_experts_timed is
+ * glm_moe_routed_experts with a HIP event recorded on `stream` before the
+ * route plan and after each of its four stages (plan, gate/up, down, combine):
+ * events[0..4], created with glm_moe_event_create.  No reference counterpart
+ * (the reference labels its kernels for the TPU profiler, kernels/names.py). */
+int glm_moe_event_create(void** event);
+int glm_moe_event_destroy(void* event);
+int glm_moe_event_elapsed_ms(void* start, void* stop, float* ms);
+int glm_moe_routed_experts_timed(const uint16_t* hidden, int64_t tokens, int64_t hidden_size,
+                                 const int32_t* route_indices, const float* route_weights,
+                                 int32_t top_k, int32_t num_experts, int64_t intermediate,
+                                 const uint8_t* gate_bits, const float* gate_scale,
+                                 const uint8_t* up_bits, const float* up_scale,
+                                 const uint8_t* down_bits, const float* down_scale,
+                                 uint32_t flags, uint16_t* out, uint8_t* valid, void* workspace,
+                                 size_t workspace_bytes, void* const* events, void* stream);
+
+/* Synthetic FP8 expert tables for tests and benchmarks, the reference's fixture
+ * recipe (tools/equivalence/fixture.py:158-172) with 128x128 block scales:
+ * w ~ N(0, sigma) (counter-based hash + Box-Muller), scale = amax/448 per block,
+ * bits = e4m3fn(clamp(w/scale, +-448)) RNE.  bits [experts, n, k], scales
+ * [experts, n/128, k/128].  Deterministic in (seed, geometry). */
+int glm_moe_synthesize_fp8_weights(uint64_t seed, int32_t experts, int64_t n, int64_t k,
+                                   float sigma, uint8_t* bits, float* scales, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* GLM_MOE_H */

@@ -1,0 +1,435 @@
+"""GPU parity of libglm_moe against the CPU oracle (oracle/moe_oracle.py).
+
+Integer work (route grouping, panel plans, FP8 decode) must be bit-exact;
+projections and the MoE outputs must be within the north-star tolerance
+``max|y - y_ref| <= 2e-2`` and ``mean|y - y_ref| / mean|y_ref| <= 5e-3`` of the
+oracle's bf16 output (kernel primitives use the reference's own tolerances,
+tests/kernels/test_fp8_panel_matmul.py:131-137).  Every call goes through the
+C ABI of libglm_moe.so.
+"""
+
+from __future__ import annotations
+
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import moe_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+GOLDEN = Path(__file__).resolve().parent / "golden" / "toy_moe.npz"
+MAX_ABS = 2e-2
+MEAN_REL = 5e-3
+TABLE_KEYS = ("gate_bits", "gate_scale", "up_bits", "up_scale", "down_bits", "down_scale")
+
+
+def dev(a, device):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(device)
+
+
+def bf16_dev(values_f32, device):
+    return torch.from_numpy(np.ascontiguousarray(values_f32, dtype=np.float32)).to(torch.bfloat16).to(device)
+
+
+def host_f32(t):
+    return t.float().cpu().numpy()
+
+
+def bf16_bits_of(t):
+    return t.cpu().view(torch.int16).numpy().view(np.uint16)
+
+
+def assert_moe_close(got, ref, max_abs=MAX_ABS, mean_rel=MEAN_REL):
+    got = np.asarray(got, np.float64)
+    ref = np.asarray(ref, np.float64)
+    assert np.all(np.isfinite(got)), "non-finite output"
+    diff = np.abs(got - ref)
+    rel = diff.mean() / max(np.abs(ref).mean(), 1e-30)
+    assert diff.max() <= max_abs, f"max-abs {diff.max():.3e} > {max_abs}"
+    assert rel <= mean_rel, f"mean-rel {rel:.3e} > {mean_rel}"
+    return diff.max(), rel
+
+
+# ----------------------------------------------------------------------------- FP8 decode
+def test_decode_fp8_table_is_bit_exact(device):
+    from glm_moe.layers.fp8 import decode_fp8_table
+
+    rng = np.random.default_rng(1)
+    bits = np.tile(np.arange(256, dtype=np.uint8), (256, 384 // 256 + 1))[:, :384].copy()
+    rng.shuffle(bits, axis=1)
+    scale = rng.uniform(0.001, 9.0, (2, 3)).astype(np.float32)
+    scale[0, 1], scale[1, 2], scale[1, 0] = 0.0, 3.25, 1.0e-30  # zero, exact, subnormal products
+    got = decode_fp8_table(dev(bits, device), dev(scale, device))
+    ref = O.decode_fp8_table(bits, scale)
+    nan = np.isnan(ref)
+    np.testing.assert_array_equal(np.isnan(host_f32(got)), nan)
+    np.testing.assert_array_equal(bf16_bits_of(got)[~nan], O.bf16_bits(ref)[~nan])
+    # non-default blocks (reference tests/layers/moe/test_router.py:84-97)
+    small = decode_fp8_table(dev(np.full((4, 6), 0x38, np.uint8), device),
+                             dev(np.array([[1, 2], [3, 4]], np.float32), device), block_shape=(2, 3))
+    np.testing.assert_array_equal(host_f32(small), [[1, 1, 1, 2, 2, 2]] * 2 + [[3, 3, 3, 4, 4, 4]] * 2)
+
+
+# ----------------------------------------------------------------------------- route grouping
+ROUTE_CASES = [(rows, conc) for rows in (1, 17, 128, 512) for conc in (False, True)]
+
+
+@pytest.mark.parametrize("rows,concentrated", ROUTE_CASES)
+def test_group_routes_is_bit_exact(device, rows, concentrated):
+    from glm_moe.layers.moe.routed_experts import gather_prefill_route_rows, group_prefill_routes, \
+        restore_prefill_route_rows
+
+    rng = np.random.default_rng(183)
+    count = 32 if concentrated else 256
+    ids = np.stack([rng.choice(count, 8, replace=False) for _ in range(rows)]).astype(np.int32)
+    got = group_prefill_routes(dev(ids, device))
+    ref = O.group_prefill_routes(ids)
+    np.testing.assert_array_equal(got.sorted_flat_ids.cpu().numpy(), ref.sorted_flat_ids)
+    np.testing.assert_array_equal(got.inverse_permutation.cpu().numpy(), ref.inverse_permutation)
+    np.testing.assert_array_equal(got.group_sizes.cpu().numpy(), ref.group_sizes)
+    assert bool(got.valid) is True
+    hidden = np.arange(rows * 4, dtype=np.float32).reshape(rows, 4)
+    gathered = gather_prefill_route_rows(bf16_dev(hidden, device), got, top_k=8)
+    np.testing.assert_array_equal(host_f32(gathered), O.gather_prefill_route_rows(hidden, ref, top_k=8))
+    values = np.arange(rows * 8 * 3, dtype=np.float32).reshape(rows * 8, 3)
+    restored = restore_prefill_route_rows(dev(values[ref.sorted_flat_ids], device), got, top_k=8)
+    np.testing.assert_array_equal(restored.cpu().numpy(), values.reshape(rows, 8, 3))
+
+
+@pytest.mark.parametrize("seed", [0, 1])
+def test_group_routes_zipf_8192_is_bit_exact(device, seed):
+    from glm_moe import synthetic as S
+    from glm_moe.layers.moe.routed_experts import group_prefill_routes
+
+    ids, _ = S.routes(S.CONFIGS["prefill_t8192_zipf"], seed)
+    got = group_prefill_routes(dev(ids, device))
+    ref = O.group_prefill_routes(ids)
+    np.testing.assert_array_equal(got.sorted_flat_ids.cpu().numpy(), ref.sorted_flat_ids)
+    np.testing.assert_array_equal(got.inverse_permutation.cpu().numpy(), ref.inverse_permutation)
+    np.testing.assert_array_equal(got.group_sizes.cpu().numpy(), ref.group_sizes)
+    assert int(ref.group_sizes.max()) > 1000  # the skew the config asks for
+
+
+@pytest.mark.parametrize("bad", [-1, 256, 0, 2**31 - 1])
+def test_group_routes_invalid_ids_match_reference_metadata(device, bad):
+    from glm_moe.layers.moe.routed_experts import group_prefill_routes
+
+    ids = np.tile(np.arange(8, dtype=np.int32), (3, 1))
+    ids[1, 7] = bad
+    got = group_prefill_routes(dev(ids, device))
+    ref = O.group_prefill_routes(ids)
+    assert not bool(got.valid) and not ref.valid
+    np.testing.assert_array_equal(got.sorted_flat_ids.cpu().numpy(), ref.sorted_flat_ids)
+    np.testing.assert_array_equal(got.group_sizes.cpu().numpy(), ref.group_sizes)
+
+
+# ----------------------------------------------------------------------------- panels
+def _panels_equal(got, ref):
+    np.testing.assert_array_equal(got.expert_ids.cpu().numpy(), ref.expert_ids)
+    np.testing.assert_array_equal(got.row_starts.cpu().numpy(), ref.row_starts)
+    np.testing.assert_array_equal(got.live_counts.cpu().numpy(), ref.live_counts)
+    assert int(got.active_panels) == ref.active_panels
+    np.testing.assert_array_equal(got.restore_indices.cpu().numpy(), ref.restore_indices)
+    np.testing.assert_array_equal(got.owned_rows.cpu().numpy(), ref.owned_rows)
+    assert bool(got.valid) == ref.valid
+
+
+@pytest.mark.parametrize("offset", [0, 2, 4])
+def test_build_expert_panels_is_bit_exact(device, offset):
+    from glm_moe.kernels.fp8_grouped_matmul.panels import build_expert_panels, pack_expert_panel_rows, \
+        unpack_expert_panel_rows
+
+    counts = np.array([1, 31, 32, 33, 0, 7], np.int32)
+    m = int(counts.sum())
+    got = build_expert_panels(dev(counts, device), torch.tensor(offset, dtype=torch.int32, device=device),
+                              rows=m, local_groups=2)
+    ref = O.build_expert_panels(counts, offset, rows=m, local_groups=2)
+    _panels_equal(got, ref)
+    x = np.arange(m * 4, dtype=np.float32).reshape(m, 4)
+    packed = pack_expert_panel_rows(dev(x, device), got)
+    np.testing.assert_array_equal(packed.cpu().numpy(), O.pack_expert_panel_rows(x, ref))
+    live = np.arange(32)[None, :] < ref.live_counts[:, None]
+    poisoned = torch.where(dev(live, device)[..., None], packed, torch.full_like(packed, float("nan")))
+    np.testing.assert_array_equal(unpack_expert_panel_rows(poisoned, got).cpu().numpy(),
+                                  O.unpack_expert_panel_rows(O.pack_expert_panel_rows(x, ref), ref))
+
+
+@pytest.mark.parametrize("counts,offset", [
+    ([19, 0, 0, 0], -1), ([19, 0, 0, 0], 3), ([19, 0, 0, 0], 2147483647),
+    ([19, -1, 0, 0], 0), ([18, 0, 0, 0], 0), ([2147483647, 0, 0, 0], 0), ([0, 129, 0, 0], 0),
+])
+def test_build_expert_panels_edge_cases_are_bit_exact(device, counts, offset):
+    from glm_moe.kernels.fp8_grouped_matmul.panels import build_expert_panels
+
+    rows = 129 if counts[1] == 129 else 19
+    local = 4 if rows == 129 else 2
+    c = np.array(counts, np.int32)
+    got = build_expert_panels(dev(c, device), torch.tensor(offset, dtype=torch.int32, device=device),
+                              rows=rows, local_groups=local)
+    _panels_equal(got, O.build_expert_panels(c, offset, rows=rows, local_groups=local))
+
+
+# ----------------------------------------------------------------------------- panel matmul
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_panel_matmul_matches_oracle(device, dtype):
+    from glm_moe.kernels.fp8_grouped_matmul.panel_kernel import prefill_panel_fp8_matmul
+    from glm_moe.kernels.fp8_grouped_matmul.panels import build_expert_panels
+
+    rng = np.random.default_rng(911)  # reference tests/kernels/test_fp8_panel_matmul.py:105-137
+    counts = np.array([1, 33, 7, 0], np.int32)
+    m, k, n = 41, 1152, 512
+    x = O.bf16_round(rng.normal(0, 0.2, (m, k)).astype(np.float32))
+    bits = torch.from_numpy(rng.normal(0, 0.15, (2, n, k)).astype(np.float32)).to(
+        torch.float8_e4m3fn).view(torch.uint8).numpy()
+    scales = rng.uniform(0.1, 2.0, (2, 4, 9)).astype(np.float32)
+    scales[0, 1, 8] = 0
+    scales[1, 3, 8] = 3.25
+    plan = build_expert_panels(dev(counts, device), torch.tensor(1, dtype=torch.int32, device=device), rows=m,
+                               local_groups=2)
+    got, ok = prefill_panel_fp8_matmul(bf16_dev(x, device), dev(bits, device), dev(scales, device), plan,
+                                       result_dtype=dtype)
+    assert bool(ok) and got.dtype == dtype
+    name = "float32" if dtype == torch.float32 else "bfloat16"
+    ref, _ = O.panel_fp8_matmul(x, bits, scales, O.build_expert_panels(counts, 1, rows=m, local_groups=2),
+                                result_dtype=name)
+    actual = host_f32(got)
+    owned = np.zeros(m, bool)
+    owned[1:41] = True
+    np.testing.assert_array_equal(actual[~owned], 0)
+    if dtype == torch.float32:
+        np.testing.assert_allclose(actual, ref, rtol=1e-5, atol=1e-5)
+    else:
+        np.testing.assert_allclose(actual, ref, rtol=2**-7, atol=2**-9)
+
+
+def test_panel_matmul_closed_form_and_invalid_plan(device):
+    from glm_moe.kernels.fp8_grouped_matmul.panel_kernel import prefill_panel_fp8_matmul
+    from glm_moe.kernels.fp8_grouped_matmul.panels import build_expert_panels
+
+    zero = torch.tensor(0, dtype=torch.int32, device=device)
+    plan = build_expert_panels(dev(np.array([0, 129, 0, 0], np.int32), device), zero, rows=129, local_groups=4)
+    x = torch.ones((129, 128), dtype=torch.bfloat16, device=device)
+    w = torch.full((4, 256, 128), 0x38, dtype=torch.uint8, device=device)  # 1.0
+    s = torch.ones((4, 2, 1), dtype=torch.float32, device=device)
+    s[1, 1, 0] = 0
+    value, ok = prefill_panel_fp8_matmul(x, w, s, plan)
+    assert bool(ok)
+    v = host_f32(value)
+    np.testing.assert_array_equal(v[:, :128], 128)
+    np.testing.assert_array_equal(v[:, 128:], 0)
+    # invalid metadata: no work at all, even with NaN operands (test_fp8_panel_matmul.py:53-78)
+    m = 19
+    xn = torch.full((m, 128), float("nan"), dtype=torch.bfloat16, device=device)
+    wn = torch.full((2, 256, 128), 127, dtype=torch.uint8, device=device)
+    sn = torch.full((2, 2, 1), float("nan"), dtype=torch.float32, device=device)
+    for counts, offset in (([19, 0, 0, 0], 2), ([19, 0, 0, 0], -1), ([18, 0, 0, 0], 0)):
+        p = build_expert_panels(dev(np.array(counts, np.int32), device),
+                                torch.tensor(offset, dtype=torch.int32, device=device), rows=m, local_groups=2)
+        value, ok = prefill_panel_fp8_matmul(xn, wn, sn, p)
+        np.testing.assert_array_equal(host_f32(value), 0)
+        assert bool(ok) == (offset == 2)
+
+
+# ----------------------------------------------------------------------------- routed projection
+@pytest.mark.parametrize("tables", [1, 2])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_routed_projection_matches_oracle(device, tables, dtype):
+    from glm_moe.kernels.fp8_grouped_matmul.kernel import RoutedProjectionConfig, fp8_routed_projection
+
+    rng = np.random.default_rng(41)
+    e, n, k, slots = 8, 512, 1152, 8
+    x = O.bf16_round(rng.normal(0, 0.2, (slots, k)).astype(np.float32))
+    pairs = []
+    for _ in range(tables):
+        bits = torch.from_numpy(rng.normal(0, 0.15, (e, n, k)).astype(np.float32)).to(
+            torch.float8_e4m3fn).view(torch.uint8).numpy()
+        scales = rng.uniform(0.1, 2.0, (e, n // 128, k // 128)).astype(np.float32)
+        pairs.append((bits, scales))
+    ids = np.array([3, -2, 9, 1, 0, 7, 7, 5], np.int32)
+    owned = np.array([True, True, True, False, True, True, False, True])
+    got = fp8_routed_projection(
+        bf16_dev(x, device), tuple((dev(b, device), dev(s, device)) for b, s in pairs), dev(ids, device),
+        dev(owned, device), config=RoutedProjectionConfig(output_tile=256, contraction_tile=128), result_dtype=dtype)
+    name = "float32" if dtype == torch.float32 else "bfloat16"
+    ref = O.routed_projection(x, tuple(pairs), ids, owned, result_dtype=name)
+    actual = host_f32(got)
+    np.testing.assert_array_equal(actual[~owned], 0)
+    if dtype == torch.float32:
+        np.testing.assert_allclose(actual, ref, rtol=1e-5, atol=1e-5)
+    else:
+        np.testing.assert_allclose(actual, ref, rtol=2**-7, atol=2**-9)
+
+
+# ----------------------------------------------------------------------------- routed experts
+@pytest.fixture(scope="module")
+def golden():
+    with np.load(GOLDEN, allow_pickle=False) as data:
+        return {k: data[k] for k in data.files}
+
+
+def _device_tables(tables, device):
+    return {k: dev(tables[k], device) for k in TABLE_KEYS}
+
+
+def test_routed_experts_toy_golden(device, golden):
+    from glm_moe.layers.moe.routed_experts import routed_experts
+
+    g = golden
+    x = dev(g["hidden_bits"].view(np.int16), device).view(torch.bfloat16)
+    ids, w = dev(g["route_indices"], device), dev(g["route_weights"], device)
+    t = _device_tables(g, device)
+    out, ok = routed_experts(x, ids, w, *(t[k] for k in TABLE_KEYS))
+    assert bool(ok)
+    print("toy fp32-sum:", assert_moe_close(host_f32(out), O.bf16_from_bits(g["routed_bits"])))
+    out16, _ = routed_experts(x, ids, w, *(t[k] for k in TABLE_KEYS), route_sum="bfloat16")
+    print("toy bf16-sum:", assert_moe_close(host_f32(out16), O.bf16_from_bits(g["routed_bf16sum_bits"])))
+
+
+def test_layers_toy_golden(device, golden):
+    from glm_moe.contracts import single_gpu_contract
+    from glm_moe.layers.moe.routed_experts import moe_grouped_routes, prefill_moe_from_routes
+
+    g = golden
+    contract = single_gpu_contract(hidden_size=256, intermediate_size=256, num_experts=8, top_k=2)
+    x = dev(g["hidden_bits"].view(np.int16), device).view(torch.bfloat16)
+    ids, w = dev(g["route_indices"], device), dev(g["route_weights"], device)
+    t = _device_tables(g, device)
+    shared = [dev(g[k].view(np.int16), device).view(torch.bfloat16)
+              for k in ("shared_gate_bits", "shared_up_bits", "shared_down_bits")]
+    out, ok = prefill_moe_from_routes(x, ids, w, *(t[k] for k in TABLE_KEYS), *shared, contract=contract)
+    assert bool(ok)
+    print("toy prefill layer:", assert_moe_close(host_f32(out), O.bf16_from_bits(g["layer_bits"])))
+    dec = moe_grouped_routes(x[:1], ids[:1], w[:1], *(t[k] for k in TABLE_KEYS), contract=contract,
+                             shared_bf16=tuple(shared))
+    print("toy decode layer:", assert_moe_close(host_f32(dec), O.bf16_from_bits(g["decode_layer_bits"])))
+
+
+def _small_case(tokens, experts, hidden, inter, top_k, zipf, seed):
+    from glm_moe import synthetic as S
+
+    cfg = S.MoeConfig("case", tokens, experts, hidden, inter, top_k, zipf)
+    x = S.hidden_states(cfg, seed)
+    ids, w = S.routes(cfg, seed)
+    return cfg, x, ids, w, S.host_expert_tables(cfg, seed)
+
+
+@pytest.mark.parametrize("tokens,experts,hidden,inter,top_k,zipf", [
+    (3, 16, 512, 256, 4, 0.0),      # skinny (decode-like), several experts
+    (64, 32, 768, 384, 8, 0.0),     # skinny with multi-route experts
+    (512, 16, 512, 256, 8, 1.2),    # wide path, skewed: multi-tile experts
+    (300, 64, 256, 512, 6, 0.0),    # wide path, ragged tiles
+])
+def test_routed_experts_matches_oracle(device, tokens, experts, hidden, inter, top_k, zipf):
+    from glm_moe.layers.moe.routed_experts import routed_experts
+
+    cfg, x, ids, w, tables = _small_case(tokens, experts, hidden, inter, top_k, zipf, seed=tokens)
+    t = _device_tables(tables, device)
+    out, ok = routed_experts(bf16_dev(x, device), dev(ids, device), dev(w, device), *(t[k] for k in TABLE_KEYS))
+    ref, ref_ok = O.routed_experts(x, ids, w, **tables)
+    assert bool(ok) == ref_ok
+    print(cfg, assert_moe_close(host_f32(out), ref))
+
+
+def test_routed_experts_invalid_routes_follow_reference(device):
+    from glm_moe.layers.moe.routed_experts import routed_experts
+
+    cfg, x, ids, w, tables = _small_case(4, 8, 256, 256, 2, 0.0, seed=9)
+    t = _device_tables(tables, device)
+    bad = ids.copy()
+    bad[2, 1] = 99
+    args = (bf16_dev(x, device), dev(bad, device), dev(w, device), *(t[k] for k in TABLE_KEYS))
+    out, ok = routed_experts(*args)
+    ref, ref_ok = O.routed_experts(x, bad, w, **tables)
+    assert not bool(ok) and not ref_ok
+    assert_moe_close(host_f32(out), ref)
+    out, _ = routed_experts(*args, drop_unowned=True, check_weights=False, route_sum="bfloat16")
+    ref, _ = O.routed_experts(x, bad, w, **tables, drop_unowned=True, check_weights=False, route_sum="bfloat16")
+    assert_moe_close(host_f32(out), ref)
+    dup = ids.copy()
+    dup[0, 1] = dup[0, 0]
+    out, ok = routed_experts(bf16_dev(x, device), dev(dup, device), dev(w, device), *(t[k] for k in TABLE_KEYS))
+    ref, ref_ok = O.routed_experts(x, dup, w, **tables)
+    assert not bool(ok) and not ref_ok
+    assert_moe_close(host_f32(out), ref)
+    neg = w.copy()
+    neg[1, 0] = float("nan")
+    _, ok = routed_experts(bf16_dev(x, device), dev(ids, device), dev(neg, device), *(t[k] for k in TABLE_KEYS))
+    assert not bool(ok)
+
+
+# ----------------------------------------------------------------------------- production shapes
+@pytest.fixture(scope="module")
+def production_tables(device):
+    from glm_moe import synthetic as S
+
+    tables = S.device_expert_tables(S.CONFIGS["decode_t1"], seed=0, device=device)
+    torch.cuda.synchronize()
+    yield tables
+    del tables
+    torch.cuda.empty_cache()
+
+
+def _subproblem(tables, ids):
+    """Host copies of the selected experts, renumbered 0..D-1, and the remapped ids."""
+    used = np.unique(ids.reshape(-1))
+    remap = {int(e): i for i, e in enumerate(used)}
+    index = torch.as_tensor(used, dtype=torch.long, device=tables["gate_bits"].device)
+    host = {k: tables[k].index_select(0, index).cpu().numpy() for k in TABLE_KEYS}
+    return host, np.vectorize(remap.get)(ids).astype(np.int32)
+
+
+def test_synthetic_weights_follow_the_recipe(device, production_tables):
+    bits = production_tables["gate_bits"][:2].cpu().numpy()
+    scales = production_tables["gate_scale"][:2].cpu().numpy()
+    assert not np.any((bits & 0x7F) == 0x7F)  # finite encodings only
+    w = O.decode_fp8_table(bits, scales)
+    assert abs(float(w.std()) - 0.02) < 0.002 and abs(float(w.mean())) < 1e-3
+    # every block's largest magnitude decodes to ~448 * scale (scale = amax / 448)
+    blocks = np.abs(O.fp8_e4m3fn_table()[bits]).reshape(2, 16, 128, 48, 128).max(axis=(2, 4))
+    assert np.all(blocks >= 416)
+
+
+@pytest.mark.parametrize("name", ["decode_t1", "decode_t4"])
+def test_decode_production_shape_matches_oracle(device, production_tables, name):
+    from glm_moe import synthetic as S
+    from glm_moe.layers.moe.routed_experts import routed_experts
+
+    cfg = S.CONFIGS[name]
+    x = S.hidden_states(cfg, 3)
+    ids, w = S.routes(cfg, 3)
+    t = production_tables
+    out, ok = routed_experts(bf16_dev(x, device), dev(ids, device), dev(w, device), *(t[k] for k in TABLE_KEYS))
+    host, local_ids = _subproblem(t, ids)
+    ref, _ = O.routed_experts(x, local_ids, w, **host)
+    assert bool(ok)
+    print(name, assert_moe_close(host_f32(out), ref))
+    again, _ = routed_experts(bf16_dev(x, device), dev(ids, device), dev(w, device), *(t[k] for k in TABLE_KEYS))
+    np.testing.assert_array_equal(bf16_bits_of(again), bf16_bits_of(out))  # deterministic
+
+
+@pytest.mark.parametrize("name", ["prefill_t2048", "prefill_t8192_zipf"])
+def test_prefill_production_shape_sampled_tokens(device, production_tables, name):
+    """Full-size prefill; each output row depends only on its token's routes, so
+    the oracle checks a sample of rows exactly, and the whole output is checked
+    for finiteness and run-to-run bit equality."""
+    from glm_moe import synthetic as S
+    from glm_moe.layers.moe.routed_experts import routed_experts
+
+    cfg = S.CONFIGS[name]
+    x = S.hidden_states(cfg, 5)
+    ids, w = S.routes(cfg, 5)
+    t = production_tables
+    args = (bf16_dev(x, device), dev(ids, device), dev(w, device), *(t[k] for k in TABLE_KEYS))
+    out, ok = routed_experts(*args)
+    assert bool(ok)
+    full = host_f32(out)
+    assert np.all(np.isfinite(full))
+    rows = np.random.default_rng(0).choice(cfg.tokens, 6, replace=False)
+    host, local_ids = _subproblem(t, ids[rows])
+    ref, _ = O.routed_experts(x[rows], local_ids, w[rows], **host)
+    print(name, assert_moe_close(full[rows], ref))
+    again, _ = routed_experts(*args)
+    np.testing.assert_array_equal(bf16_bits_of(again), bf16_bits_of(out))

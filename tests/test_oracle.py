@@ -1,0 +1,344 @@
+"""Pins of the CPU oracle (oracle/moe_oracle.py) against the reference's own
+known answers, independent libraries, closed forms and brute force.
+
+Each check is chosen so that a plausible mistake in the oracle (a dropped
+term, a wrong index or sign, a transposed operand) fails it.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import moe_oracle as O
+
+
+# ----------------------------------------------------------------------------- scalar formats
+def test_e4m3fn_table_matches_torch_for_every_bit_pattern():
+    ours = O.fp8_e4m3fn_table()
+    theirs = torch.arange(256, dtype=torch.uint8).view(torch.float8_e4m3fn).float().numpy()
+    nan = np.isnan(theirs)
+    np.testing.assert_array_equal(np.isnan(ours), nan)
+    np.testing.assert_array_equal(ours[~nan], theirs[~nan])
+
+
+def test_e4m3fn_known_answers():
+    t = O.fp8_e4m3fn_table()
+    # 0x38 = 1.0 (reference tests/layers/test_fp8.py:115-119), max finite 448, NaN codes
+    assert t[0x38] == 1.0 and t[0xB8] == -1.0
+    assert t[0x7E] == 448.0 and t[0xFE] == -448.0
+    assert np.isnan(t[0x7F]) and np.isnan(t[0xFF])
+    assert t[0x01] == 2.0**-9 and t[0x07] == 7 * 2.0**-9  # subnormals m * 2^-9
+    assert t[0x08] == 2.0**-6  # smallest normal
+    assert t[0x00] == 0.0 and np.signbit(t[0x80])
+    assert int(np.isnan(t).sum()) == 2
+
+
+def test_bf16_round_matches_torch_cast():
+    rng = np.random.default_rng(5)
+    x = np.concatenate([
+        rng.standard_normal(20000).astype(np.float32) * 10.0 ** rng.integers(-30, 30, 20000),
+        # exact ties: bf16 mantissa + half an ulp, both parities
+        np.array([1.0 + 2**-8, 1.0 + 3 * 2**-8, -(1.0 + 2**-8), 3.0e38, -3.39e38, 1e-40, 0.0, -0.0],
+                 np.float32),
+        np.array([np.inf, -np.inf], np.float32),
+    ]).astype(np.float32)
+    ours = O.bf16_round(x)
+    theirs = torch.from_numpy(x).to(torch.bfloat16).float().numpy()
+    np.testing.assert_array_equal(ours, theirs)
+    assert np.isnan(O.bf16_round(np.array([np.nan], np.float32)))[0]
+    # tie to even: 1 + 2^-8 lies between 1 and 1 + 2^-7 and rounds to 1
+    assert O.bf16_round(np.float32(1.0 + 2**-8))[()] == 1.0
+    assert O.bf16_round(np.float32(1.0 + 3 * 2**-8))[()] == 1.0 + 2**-6
+
+
+def test_decode_uses_checkpoint_out_in_blocks():
+    # reference tests/layers/moe/test_router.py:84-97: block (r, c) scales rows r and columns c
+    bits = np.full((4, 6), 0x38, np.uint8)  # all 1.0
+    scale = np.array([[1.0, 2.0], [3.0, 4.0]], np.float32)
+    got = O.decode_fp8_table(bits, scale, block_shape=(2, 3))
+    expected = np.array([[1, 1, 1, 2, 2, 2], [1, 1, 1, 2, 2, 2], [3, 3, 3, 4, 4, 4], [3, 3, 3, 4, 4, 4]],
+                        np.float32)
+    np.testing.assert_array_equal(got, expected)
+
+
+def test_decode_is_one_f32_product_then_one_bf16_rounding():
+    # independent of the oracle: FP64 product (exact: 4 + 24 bits) -> f32 -> bf16 via torch
+    # (tests/reference/independent.py:78-88 double rounding argument)
+    rng = np.random.default_rng(11)
+    bits = rng.integers(0, 256, (256, 384), dtype=np.uint8)
+    bits[(bits & 0x7F) == 0x7F] = 0x3C
+    scale = rng.uniform(0.01, 7.0, (2, 3)).astype(np.float32)
+    values = torch.from_numpy(bits).view(torch.float8_e4m3fn).double().numpy()
+    expanded = np.repeat(np.repeat(scale.astype(np.float64), 128, 0), 128, 1)
+    expected = torch.from_numpy((values * expanded).astype(np.float32)).to(torch.bfloat16).float().numpy()
+    np.testing.assert_array_equal(O.decode_fp8_table(bits, scale), expected)
+
+
+# ----------------------------------------------------------------------------- route grouping
+def _brute_stable_sort(keys: list[int]) -> list[int]:
+    order: list[int] = []
+    for i, key in enumerate(keys):  # insertion sort: stable by construction
+        j = len(order)
+        while j > 0 and keys[order[j - 1]] > key:
+            j -= 1
+        order.insert(j, i)
+    return order
+
+
+@pytest.mark.parametrize("rows", [1, 17, 128])
+@pytest.mark.parametrize("concentrated", [False, True])
+def test_group_routes_is_the_stable_counting_sort(rows, concentrated):
+    rng = np.random.default_rng(183)  # reference tests/layers/moe/test_routed_experts.py:15-37
+    count = 32 if concentrated else 256
+    ids = np.stack([rng.choice(count, 8, replace=False) for _ in range(rows)]).astype(np.int32)
+    r = O.group_prefill_routes(ids)
+    assert r.valid
+    flat = ids.reshape(-1).tolist()
+    assert r.sorted_flat_ids.tolist() == _brute_stable_sort(flat)
+    counts = [0] * 256
+    for e in flat:
+        counts[e] += 1
+    assert r.group_sizes.tolist() == counts
+    assert all(r.sorted_flat_ids[r.inverse_permutation[i]] == i for i in range(len(flat)))
+    if concentrated:
+        assert int(r.group_sizes[32:].sum()) == 0
+    values = np.arange(rows * 8 * 3, dtype=np.float32).reshape(rows * 8, 3)
+    restored = O.restore_prefill_route_rows(values[r.sorted_flat_ids], r, top_k=8)
+    np.testing.assert_array_equal(restored, values.reshape(rows, 8, 3))
+    hidden = np.arange(rows * 4, dtype=np.float32).reshape(rows, 4)
+    np.testing.assert_array_equal(O.gather_prefill_route_rows(hidden, r, top_k=8),
+                                  hidden[np.asarray(_brute_stable_sort(flat)) // 8])
+
+
+@pytest.mark.parametrize("bad", [-1, 256, 0])
+def test_invalid_or_duplicate_routes_are_not_admitted(bad):
+    # reference tests/layers/moe/test_routed_experts.py:40-44; invalid ids count as expert 0
+    ids = np.arange(8, dtype=np.int32)[None, :].copy()
+    ids[0, 7] = bad
+    r = O.group_prefill_routes(ids)
+    assert not r.valid
+    assert int(r.group_sizes.sum()) == 8
+    if bad != 0:
+        assert r.group_sizes[0] == 2 and r.sorted_flat_ids.tolist()[:2] == [0, 7]
+
+
+def test_wrong_route_dtype_is_rejected():
+    with pytest.raises(ValueError, match="int32"):
+        O.group_prefill_routes(np.zeros((2, 8), np.float32))
+
+
+# ----------------------------------------------------------------------------- panels
+@pytest.mark.parametrize("offset", [0, 2, 4])
+def test_panels_restore_every_owned_row_once(offset):
+    # reference tests/kernels/test_fp8_panel_matmul.py:31-50
+    counts = np.array([1, 31, 32, 33, 0, 7], np.int32)
+    m = int(counts.sum())
+    x = np.arange(m * 3, dtype=np.float32).reshape(m, 3)
+    plan = O.build_expert_panels(counts, offset, rows=m, local_groups=2)
+    assert plan.valid
+    assert plan.active_panels == sum((int(c) + 31) // 32 for c in counts[offset:offset + 2])
+    packed = O.pack_expert_panel_rows(x, plan)
+    live = np.arange(32)[None, :] < plan.live_counts[:, None]
+    np.testing.assert_array_equal(packed[~live], 0)
+    group = np.repeat(np.arange(6), counts)
+    owned = (group >= offset) & (group < offset + 2)
+    indices = plan.restore_indices[owned]
+    assert len(np.unique(indices)) == int(counts[offset:offset + 2].sum())
+    assert live.reshape(-1)[indices].all()
+    poisoned = np.where(live[..., None], packed, np.nan)
+    np.testing.assert_array_equal(O.unpack_expert_panel_rows(poisoned, plan), np.where(owned[:, None], x, 0))
+
+
+@pytest.mark.parametrize("counts,offset", [
+    ([19, 0, 0, 0], -1), ([19, 0, 0, 0], 3), ([19, 0, 0, 0], 2147483647),
+    ([19, -1, 0, 0], 0), ([18, 0, 0, 0], 0), ([2147483647, 0, 0, 0], 0),
+])
+def test_invalid_panel_metadata_gives_no_work(counts, offset):
+    # reference tests/kernels/test_fp8_panel_matmul.py:53-78
+    plan = O.build_expert_panels(np.array(counts, np.int32), offset, rows=19, local_groups=2)
+    assert not plan.valid and plan.active_panels == 0
+    assert not plan.owned_rows.any()
+
+
+def test_panel_capacity_closed_form_and_scale_zero():
+    # reference tests/kernels/test_fp8_panel_matmul.py:140-151
+    plan = O.build_expert_panels(np.array([0, 129, 0, 0], np.int32), 0, rows=129, local_groups=4)
+    assert plan.active_panels == 5
+    np.testing.assert_array_equal(plan.live_counts[:5], [32, 32, 32, 32, 1])
+    x = np.ones((129, 128), np.float32)
+    w = np.full((4, 256, 128), 0x38, np.uint8)
+    s = np.ones((4, 2, 1), np.float32)
+    s[1, 1, 0] = 0
+    value, ok = O.panel_fp8_matmul(x, w, s, plan)
+    assert ok
+    np.testing.assert_array_equal(value[:, :128], 128)
+    np.testing.assert_array_equal(value[:, 128:], 0)
+
+
+def _fp64_dequant_dot(x, bits, scales):
+    """FP64 brute force: whole-K contraction (a different order from the oracle's blocks)."""
+    w = torch.from_numpy(bits).view(torch.float8_e4m3fn).double().numpy()
+    expanded = np.repeat(np.repeat(scales.astype(np.float64), 128, -2), 128, -1)
+    wq = torch.from_numpy((w * expanded).astype(np.float32)).to(torch.bfloat16).double().numpy()
+    return x.astype(np.float64) @ wq.T
+
+
+@pytest.mark.parametrize("dtype", ["float32", "bfloat16"])
+def test_panel_matmul_matches_fp64_brute_force(dtype):
+    # the reference's random case (tests/kernels/test_fp8_panel_matmul.py:105-137)
+    rng = np.random.default_rng(911)
+    counts = np.array([1, 33, 7, 0], np.int32)
+    m, k, n = 41, 1152, 512
+    x = O.bf16_round(rng.normal(0, 0.2, (m, k)).astype(np.float32))
+    bits = torch.from_numpy(rng.normal(0, 0.15, (2, n, k)).astype(np.float32)).to(
+        torch.float8_e4m3fn).view(torch.uint8).numpy()
+    scales = rng.uniform(0.1, 2.0, (2, 4, 9)).astype(np.float32)
+    scales[0, 1, 8] = 0
+    scales[1, 3, 8] = 3.25
+    plan = O.build_expert_panels(counts, 1, rows=m, local_groups=2)
+    value, ok = O.panel_fp8_matmul(x, bits, scales, plan, result_dtype=dtype)
+    assert ok
+    group = np.repeat(np.arange(4), counts) - 1
+    owned = (group >= 0) & (group < 2)
+    assert int(owned.sum()) == 40
+    np.testing.assert_array_equal(value[~owned], 0)
+    expected = np.zeros((m, n))
+    for row in np.nonzero(owned)[0]:
+        expected[row] = _fp64_dequant_dot(x[row:row + 1], bits[group[row]], scales[group[row]])[0]
+    if dtype == "float32":
+        np.testing.assert_allclose(value, expected, rtol=1e-5, atol=1e-5)
+    else:
+        np.testing.assert_allclose(value, expected, rtol=2**-7, atol=2**-9)
+    # a transposed scale table must be caught by the same check
+    wrong = _fp64_dequant_dot(x[1:2], bits[0], scales[0][::-1].copy())[0]
+    assert np.max(np.abs(wrong - expected[1])) > 1e-2
+
+
+def test_routed_projection_clips_ids_and_zeroes_unowned_slots():
+    rng = np.random.default_rng(3)
+    e, n, k = 4, 256, 384
+    x = O.bf16_round(rng.standard_normal((5, k)).astype(np.float32))
+    tables = []
+    for _ in range(2):
+        bits = rng.integers(0, 0x7E, (e, n, k), dtype=np.uint8)
+        scales = rng.uniform(0.001, 0.01, (e, n // 128, k // 128)).astype(np.float32)
+        tables.append((bits, scales))
+    ids = np.array([3, -2, 9, 1, 0], np.int32)
+    owned = np.array([True, True, True, False, True])
+    out = O.routed_projection(x, tuple(tables), ids, owned)
+    assert out.shape == (5, 2, n)
+    np.testing.assert_array_equal(out[3], 0)
+    for s, expert in ((0, 3), (1, 0), (2, 3), (4, 0)):
+        for t in range(2):
+            ref = _fp64_dequant_dot(x[s:s + 1], tables[t][0][expert], tables[t][1][expert])[0]
+            np.testing.assert_allclose(out[s, t], ref, rtol=1e-5, atol=1e-4)
+
+
+# ----------------------------------------------------------------------------- SwiGLU and routed experts
+def test_swiglu_rounds_after_every_op():
+    g = O.bf16_round(np.linspace(-8, 8, 4097).astype(np.float32))
+    u = O.bf16_round(np.float32(1.0) + np.zeros_like(g))
+    np.testing.assert_array_equal(O.swiglu_bf16(g, np.zeros_like(g)), 0)
+    s = torch.sigmoid(torch.from_numpy(g).to(torch.bfloat16))  # torch: f32 math, one rounding
+    expected = (torch.from_numpy(g).to(torch.bfloat16) * s).float().numpy()
+    np.testing.assert_array_equal(O.swiglu_bf16(g, u), expected)
+
+
+def _fp64_routed(x, ids, w, tables, route_sum_scale=1.0):
+    """tests/reference/independent.py:257-287 form: FP64 everywhere after the bf16 weight decode."""
+    def dq(bits, scales):
+        v = torch.from_numpy(bits).view(torch.float8_e4m3fn).double().numpy()
+        ex = np.repeat(np.repeat(scales.astype(np.float64), 128, -2), 128, -1)
+        return torch.from_numpy((v * ex).astype(np.float32)).to(torch.bfloat16).double().numpy()
+    out = np.zeros((x.shape[0], x.shape[1]))
+    for t in range(ids.shape[0]):
+        for s in range(ids.shape[1]):
+            e = ids[t, s]
+            gate = dq(tables["gate_bits"][e], tables["gate_scale"][e]) @ x[t]
+            up = dq(tables["up_bits"][e], tables["up_scale"][e]) @ x[t]
+            act = gate / (1 + np.exp(-gate)) * up
+            out[t] += w[t, s] * route_sum_scale * (dq(tables["down_bits"][e], tables["down_scale"][e]) @ act)
+    return out
+
+
+def test_routed_experts_matches_fp64_restatement_and_catches_planted_mistakes():
+    from glm_moe import synthetic as S
+
+    cfg = S.CONFIGS["toy"]
+    x = S.hidden_states(cfg, 0).astype(np.float64)
+    ids, w = S.routes(cfg, 0)
+    tables = S.host_expert_tables(cfg, 0)
+    got, ok = O.routed_experts(x, ids, w, **tables)
+    assert ok
+    ref = _fp64_routed(x, ids, w, tables)
+    bound = 0.015 * np.abs(ref).max()  # tests/reference/test_reference_consistency.py:659-742
+    assert np.abs(got - ref).max() <= bound
+    # planted mistakes in the oracle's arithmetic must exceed the same bound
+    dropped_weight = _fp64_routed(x, ids, np.ones_like(w), tables)
+    assert np.abs(dropped_weight - ref).max() > bound
+    swapped = dict(tables, gate_bits=tables["up_bits"], up_bits=tables["gate_bits"],
+                   gate_scale=tables["up_scale"], up_scale=tables["gate_scale"])
+    assert np.abs(_fp64_routed(x, ids, w, swapped) - ref).max() > bound
+    # the bf16 route sum stays within the same bound
+    got_bf16, _ = O.routed_experts(x, ids, w, **tables, route_sum="bfloat16")
+    assert np.abs(got_bf16 - ref).max() <= bound
+
+
+def test_routed_experts_invalid_routes_follow_the_reference():
+    from glm_moe import synthetic as S
+
+    cfg = S.CONFIGS["toy"]
+    x = S.hidden_states(cfg, 1)
+    ids, w = S.routes(cfg, 1)
+    tables = S.host_expert_tables(cfg, 1)
+    bad = ids.copy()
+    bad[2, 1] = 99  # out of range: computed as expert 0, health false
+    out, ok = O.routed_experts(x, bad, w, **tables)
+    assert not ok
+    safe = bad.copy()
+    safe[2, 1] = 0
+    ref, _ = O.routed_experts(x, safe, w, **tables)
+    np.testing.assert_array_equal(out, ref)
+    dropped, _ = O.routed_experts(x, bad, w, **tables, drop_unowned=True)
+    zero_w = w.copy()
+    zero_w[2, 1] = 0.0
+    ref_drop, _ = O.routed_experts(x, ids, zero_w, **tables)
+    np.testing.assert_array_equal(dropped[[0, 1, 3]], ref_drop[[0, 1, 3]])
+    neg = w.copy()
+    neg[0, 0] = -0.5
+    assert not O.routed_experts(x, ids, neg, **tables)[1]
+    assert O.routed_experts(x, ids, neg, **tables, check_weights=False)[1]
+
+
+# ----------------------------------------------------------------------------- router
+def test_noaux_bias_selects_but_does_not_weight():
+    # reference tests/layers/moe/test_router.py:100-107
+    logits = np.array([[3.0, 2.0, 1.0, 0.0]], np.float32)
+    bias = np.array([0.0, 0.0, 100.0, 99.0], np.float32)
+    idx, w = O.route_glm_noaux_tc_logits(logits, bias, top_k=2)
+    np.testing.assert_array_equal(idx, [[2, 3]])
+    s = 1 / (1 + np.exp(-np.array([1.0, 0.0])))
+    np.testing.assert_allclose(w[0], s / s.sum(), rtol=1e-6)
+
+
+def test_router_ties_choose_lowest_expert_ids():
+    # reference tests/layers/moe/test_router.py:110-114
+    idx, w = O.route_glm_noaux_tc_logits(np.zeros((1, 16), np.float32), np.zeros(16, np.float32), top_k=8)
+    np.testing.assert_array_equal(idx, [list(range(8))])
+    np.testing.assert_array_equal(w, np.full((1, 8), 0.125, np.float32))
+
+
+def test_synthetic_router_agrees_with_oracle_router():
+    from glm_moe import synthetic as S
+
+    for name in ("toy", "decode_t4", "prefill_t8192_zipf"):
+        cfg = S.CONFIGS[name]
+        if cfg.tokens > 64:
+            cfg = S.MoeConfig(cfg.name, 64, cfg.experts, cfg.hidden, cfg.intermediate, cfg.top_k, cfg.zipf)
+        logits = S.router_logits(cfg, 7)
+        a = S.noaux_tc_route(logits, None, cfg.top_k)
+        b = O.route_glm_noaux_tc_logits(logits, np.zeros(cfg.experts, np.float32), cfg.top_k)
+        np.testing.assert_array_equal(a[0], b[0])
+        np.testing.assert_array_equal(a[1], b[1])
