@@ -22,7 +22,7 @@ __global__ void decode_fp8_table_kernel(const uint8_t* bits, const float* scale,
   }
 }
 
-// dst[i] = mask[i] ? src[clamp(index[i], 0, src_rows - 1) / div] : 0, row-wise (dwords).
+// dst[i] = mask[i] ? src[clamp(index[i] / div, 0, src_rows - 1)] : 0, row-wise (dwords).
 __global__ void gather_rows_kernel(const uint32_t* src, int64_t src_rows, int64_t row_words,
                                    const int32_t* index, int32_t div, const uint8_t* mask, int64_t n,
                                    uint32_t* dst) {
@@ -34,9 +34,8 @@ __global__ void gather_rows_kernel(const uint32_t* src, int64_t src_rows, int64_
     const bool keep = mask == nullptr || mask[row] != 0;
     uint32_t v = 0;
     if (keep) {
-      int64_t s = index[row];
+      int64_t s = index[row] / div;
       s = s < 0 ? 0 : (s >= src_rows ? src_rows - 1 : s);
-      s /= div;
       v = src[s * row_words + w];
     }
     dst[i] = v;

@@ -69,7 +69,7 @@ int glm_moe_group_routes(const int32_t* route_indices, int64_t tokens, int32_t t
 
 /* Replaces glm_tpu/layers/moe/routed_experts.py:167-183 gather_prefill_route_rows /
  * restore_prefill_route_rows and panels.py:98-104 unpack_expert_panel_rows:
- * dst[i] = mask[i] ? src[clamp(index[i], 0, src_rows - 1) / div] : 0, whole rows of
+ * dst[i] = mask[i] ? src[clamp(index[i] / div, 0, src_rows - 1)] : 0, whole rows of
  * row_bytes (a multiple of 4).  mask may be NULL (keep every row). */
 int glm_moe_gather_rows(const void* src, int64_t src_rows, int64_t row_bytes,
                         const int32_t* index, int32_t div, const uint8_t* mask, int64_t rows,

@@ -91,7 +91,7 @@ def test_group_routes_is_bit_exact(device, rows, concentrated):
     np.testing.assert_array_equal(got.inverse_permutation.cpu().numpy(), ref.inverse_permutation)
     np.testing.assert_array_equal(got.group_sizes.cpu().numpy(), ref.group_sizes)
     assert bool(got.valid) is True
-    hidden = np.arange(rows * 4, dtype=np.float32).reshape(rows, 4)
+    hidden = O.bf16_round(np.arange(rows * 4, dtype=np.float32).reshape(rows, 4))
     gathered = gather_prefill_route_rows(bf16_dev(hidden, device), got, top_k=8)
     np.testing.assert_array_equal(host_f32(gathered), O.gather_prefill_route_rows(hidden, ref, top_k=8))
     values = np.arange(rows * 8 * 3, dtype=np.float32).reshape(rows * 8, 3)
