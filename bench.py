@@ -195,8 +195,12 @@ def main():
     torch.cuda.synchronize()
     work = Workload(cfg, tables, device)
     print(f"[bench] timing {args.steps} steps after {args.warmup} warmups", file=sys.stderr, flush=True)
-    ms, stages, order = run_steps(work, args.steps, args.warmup)
+    # headline: a clean loop (no events between the kernels); per-kernel times: a
+    # second loop with HIP events recorded on the launch stream around every stage
+    ms, _, _ = run_steps(work, args.steps, args.warmup, with_stage_events=False)
+    ms_ev, stages, order = run_steps(work, args.steps, args.warmup)
     head = summarize(work, ms, stages, order)
+    head["us_per_layer_with_stage_events"] = ms_ev * 1e3
 
     decode_like = cfg.tokens * cfg.top_k <= 8 * cfg.experts
     if decode_like:
@@ -216,7 +220,8 @@ def main():
         scfg = S.CONFIGS[name]
         print(f"[bench] secondary {name}", file=sys.stderr, flush=True)
         swork = Workload(scfg, tables, device, rotations=8)
-        sms, sstages, sorder = run_steps(swork, args.secondary_steps, 3)
+        sms, _, _ = run_steps(swork, args.secondary_steps, 3, with_stage_events=False)
+        _, sstages, sorder = run_steps(swork, args.secondary_steps, 3)
         s = summarize(swork, sms, sstages, sorder)
         s["hbm_frac"] = s["layer_hbm_gbs"] / HBM_PEAK_GBS
         s["bf16_mfma_frac"] = s["layer_tflops"] / BF16_PEAK_TFLOPS
@@ -252,6 +257,7 @@ def main():
         "layer_hbm_gbs": head["layer_hbm_gbs"],
         "layer_hbm_frac": head["layer_hbm_gbs"] / HBM_PEAK_GBS,
         "stage_us": head["stage_us"],
+        "us_per_layer_with_stage_events": head["us_per_layer_with_stage_events"],
         "distinct_experts": head["distinct_experts"],
         "roofline": roofline,
         "cpu_baseline": baseline,

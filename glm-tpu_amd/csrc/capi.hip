@@ -53,9 +53,11 @@ int key_bits_for(int experts) {
   return bits;
 }
 
-// Shape family of the grouped GEMM for a route set: the skinny split-K kernel
-// while experts see few routes each (decode), the wide one otherwise.
+// Shape family of the grouped GEMM for a route set: split-K kernels while
+// experts see few routes each (decode: <= 4 routes per tile; up to 8 routes
+// per expert on average: <= 16), the wide LDS-tiled kernel otherwise.
 int routed_shape(int64_t routes, int32_t experts) {
+  if (routes <= (int64_t)experts) return kShapeDecode;
   return routes <= 8 * (int64_t)experts ? kShapeSkinny : kShapeWide;
 }
 
@@ -135,6 +137,37 @@ int routed_experts_impl(const uint16_t* hidden, int64_t tokens, int64_t hidden_s
 
   int st = record(events, 0, stream);
   if (st) return st;
+
+  if (n <= kMaxDecodeRoutes) {
+    // decode: two kernels that group the routes themselves and fuse the combine
+    DecodeArgs d{};
+    d.ids = route_indices;
+    d.weights = route_weights;
+    d.routes = (int32_t)n;
+    d.top_k = top_k;
+    d.experts = num_experts;
+    d.key_bits = key_bits_for(num_experts);
+    d.drop_unowned = (flags & GLM_MOE_DROP_UNOWNED) ? 1 : 0;
+    d.check_weights = (flags & GLM_MOE_CHECK_WEIGHTS) ? 1 : 0;
+    d.bf16_sum = (flags & GLM_MOE_ROUTE_SUM_BF16) ? 1 : 0;
+    d.hidden_in = hidden;
+    d.hidden = (int32_t)hidden_size;
+    d.intermediate = (int32_t)intermediate;
+    d.gate_bits = gate_bits;
+    d.gate_scale = gate_scale;
+    d.up_bits = up_bits;
+    d.up_scale = up_scale;
+    d.down_bits = down_bits;
+    d.down_scale = down_scale;
+    d.act = act;
+    d.out = out;
+    d.valid = valid;
+    d.between_event = events ? events[2] : nullptr;
+    if ((st = record(events, 1, stream))) return st;
+    GLM_HIP(launch_decode_routed(d, stream), "decode launch");
+    if ((st = record(events, 3, stream))) return st;
+    return record(events, 4, stream);
+  }
 
   RoutePlanArgs p{};
   p.ids = route_indices;
@@ -415,7 +448,7 @@ int glm_moe_routed_projection(const uint16_t* lhs, int32_t slots, int64_t k, int
   g.out = out;
   g.ldo = (int64_t)tables * n;
   g.table_stride = n;
-  GLM_HIP(launch_grouped_gemm(g, kShapeSkinny, tables, result_dtype == GLM_MOE_F32 ? kEpiStoreF32 : kEpiStoreBf16, s),
+  GLM_HIP(launch_grouped_gemm(g, kShapeDecode, tables, result_dtype == GLM_MOE_F32 ? kEpiStoreF32 : kEpiStoreBf16, s),
           "routed projection launch");
   return GLM_MOE_OK;
 }

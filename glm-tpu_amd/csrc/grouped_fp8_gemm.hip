@@ -1,4 +1,5 @@
-// Route-grouped FP8 expert projection on gfx950 bf16 MFMA.
+// Route-grouped FP8 expert projection on gfx950 bf16 MFMA: the skinny
+// (decode) kernel, for work tiles of at most 4, 16 or 32 routes.
 //
 // Computes, for every work tile (expert e, sorted routes [r0, r0 + live)) and
 // every BN-row stripe of the expert's weight table,
@@ -12,33 +13,44 @@
 //   A = 16 weight rows x 32 K: lane l holds row l%16, eight K values of group l/16.
 //   B = 32 K x 16 routes:      lane l holds route l%16, the same eight K values.
 //   D = 16 weight rows x 16 routes: lane l holds rows 4*(l/16)+j, route l%16.
-// Weights are the streamed operand: every lane loads 16 contiguous e4m3 bytes
-// of its row with one 128-bit load (two loads cover a 128-wide K block, a
-// whole 128-byte line per row), decodes them in registers with the block
-// scale to bf16 and feeds them straight to the MFMA A operand; each weight
-// byte is read from HBM once per tile and decoded once.  The K index inside a
-// block is permuted identically for A and B (lane group g holds K = g*16+0..7
-// for the first MFMA and g*16+8..15 for the second), which only reorders the
-// FP32 sum inside one K block.
-// Activations (B) are gathered rows (the route's token row for gate/up, the
-// sorted activation row for down), read with 128-bit loads.
-// Epilogues fuse the bf16 SwiGLU of gate/up (routed_experts.py:102) and the
-// bf16 route weighting of down (routed_experts.py:104-105).
+// The K index inside a 128-wide block is permuted identically for A and B
+// (lane group g holds K = g*16+0..7 for the first MFMA, g*16+8..15 for the
+// second, 64+g*16+... for the third and fourth), which only reorders the FP32
+// sum inside one block.
+//
+// Weights are the streamed operand.  Each wave owns RG 16-row groups of every
+// table and a K range (WK waves split K); it streams 256-byte row segments
+// through its own swizzled LDS region (weight_stage.h), decodes each e4m3 byte
+// once with its block scale into the bf16 A operand.  The tile's activation
+// rows (B, at most XROWS routes) are staged the same way, and both operands of
+// two steps are kept in flight in one register ring, so that waiting for a
+// step never waits for a later one.  Split-K partial sums meet in LDS and are added in wave
+// order, so results are deterministic.  Epilogues fuse the bf16 SwiGLU of
+// gate/up (routed_experts.py:102) and the bf16 route weighting of down
+// (routed_experts.py:104-105).
+#include "gemm_epilogue.h"
 #include "moe_common.h"
 #include "moe_kernels.h"
+#include "weight_stage.h"
 
 namespace glm_moe {
 
 namespace {
 
-template <int TABLES, int RG, int CG>
-struct Frag {
-  f32x4 v[TABLES][RG][CG];
-};
-
-template <int TABLES, int RG, int CG, int WN, int WK, int EPI>
+// Streaming needs many resident waves: the decode shapes ask for four per SIMD
+// (at most 128 VGPRs), the wider ones for what fits.
+template <int TABLES, int RG, int XROWS, int WN, int WK, int DEPTH, int EPI>
 __global__ __launch_bounds__(64 * WN * WK) void grouped_fp8_gemm_kernel(const GroupedGemmArgs a) {
   constexpr int BN = WN * RG * 16;
+  constexpr int WAVES = WN * WK;
+  constexpr int REGIONS = TABLES * RG;       // 4 KB weight regions per wave
+  constexpr int CG = (XROWS + 15) / 16;      // 16-route column groups
+  constexpr int XI = XROWS / 4;              // activation loads per K block
+  constexpr int XBYTES = XROWS * 256;        // staged activations per K block
+  static_assert(XROWS % 4 == 0 && XROWS <= 32, "staged activation rows");
+  __shared__ __attribute__((aligned(16))) uint8_t wlds[WAVES][REGIONS][kStageBytes];
+  __shared__ __attribute__((aligned(16))) uint8_t xlds[WAVES][2][XBYTES];
+
   const int tile = blockIdx.x;
   if (tile >= a.tile_count[0]) return;
   if (a.valid != nullptr && a.valid[0] == 0) return;
@@ -47,10 +59,10 @@ __global__ __launch_bounds__(64 * WN * WK) void grouped_fp8_gemm_kernel(const Gr
   const int live = a.tile_live[tile];
   // A consistent plan always passes; a corrupt one computes nothing instead of
   // reading out of bounds.
-  if (e < 0 || e >= a.experts || r0 < 0 || live <= 0 || live > CG * 16 || r0 + live > a.rows) return;
+  if (e < 0 || e >= a.experts || r0 < 0 || live <= 0 || live > XROWS || r0 + live > a.rows) return;
 
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
   const int wn = wave % WN;
   const int wk = wave / WN;
   const int lrow = lane & 15;
@@ -58,11 +70,12 @@ __global__ __launch_bounds__(64 * WN * WK) void grouped_fp8_gemm_kernel(const Gr
   const int N = a.n;
   const int K = a.k;
   const int KB = K / kScaleBlock;
+  const int NS = (KB + 1) / 2;  // steps of two K blocks
+  const int s0 = (NS * wk) / WK;
+  const int s1 = (NS * (wk + 1)) / WK;
   const int n0 = blockIdx.y * BN + wn * RG * 16;
-  const int kb0 = (KB * wk) / WK;
-  const int kb1 = (KB * (wk + 1)) / WK;
 
-  const uint8_t* wptr[TABLES][RG];
+  WeightRows wrows[TABLES][RG];
   const float* sptr[TABLES][RG];
 #pragma unroll
   for (int t = 0; t < TABLES; ++t) {
@@ -70,96 +83,107 @@ __global__ __launch_bounds__(64 * WN * WK) void grouped_fp8_gemm_kernel(const Gr
     const float* sb = t == 0 ? a.s0 : a.s1;
 #pragma unroll
     for (int rg = 0; rg < RG; ++rg) {
-      const int row = n0 + rg * 16 + lrow;
-      wptr[t][rg] = wb + ((size_t)e * N + row) * (size_t)K + lgrp * 16;
+      wrows[t][rg] = weight_rows(wb, (int64_t)e * N + n0 + rg * 16, K, lane);
       sptr[t][rg] = sb + ((size_t)e * (N / kScaleBlock) + (n0 + rg * 16) / kScaleBlock) * KB;
     }
   }
-  const uint16_t* xptr[CG];
-  bool xok[CG];
+  // activation rows this lane loads: row 4q + lane/16 of the tile, chunk lane%16
+  const uint16_t* xsrc[XI];
+  bool xok[XI];
 #pragma unroll
-  for (int cg = 0; cg < CG; ++cg) {
-    const int col = cg * 16 + lrow;
-    xok[cg] = col < live;
-    const int r = r0 + (xok[cg] ? col : 0);
+  for (int q = 0; q < XI; ++q) {
+    const int i = 4 * q + lgrp;
+    xok[q] = i < live;
+    const int r = r0 + (xok[q] ? i : 0);
     int64_t phys = a.x_row_ids ? a.x_row_ids[r] / a.x_row_div : r;
     phys = phys < 0 ? 0 : (phys >= a.x_rows ? a.x_rows - 1 : phys);
-    xptr[cg] = a.x + (size_t)phys * K + lgrp * 16;
+    xsrc[q] = a.x + (size_t)phys * K + lrow * 8;
   }
 
-  Frag<TABLES, RG, CG> acc;
+  f32x4 acc[TABLES][RG][CG];
 #pragma unroll
   for (int t = 0; t < TABLES; ++t)
 #pragma unroll
     for (int rg = 0; rg < RG; ++rg)
 #pragma unroll
-      for (int cg = 0; cg < CG; ++cg) acc.v[t][rg][cg] = f32x4{0.f, 0.f, 0.f, 0.f};
+      for (int cg = 0; cg < CG; ++cg) acc[t][rg][cg] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  // Register double buffer: the next K block's weights and activations are in
-  // flight while the current block is decoded and multiplied.
-  u32x4 wbuf[2][TABLES][RG][2];
-  u32x4 xbuf[2][CG][4];
-  float sbuf[2][TABLES][RG];
+  uint8_t(*region)[kStageBytes] = wlds[wave];
+  uint8_t(*xregion)[XBYTES] = xlds[wave];
+  // DEPTH steps of weights and activations are in flight (in registers) while
+  // the previous one is multiplied out of LDS; both operands of a step are
+  // issued together, so waiting for a step never waits for a later one.
+  u32x4 wring[DEPTH][TABLES][RG][4];
+  u32x4 xring[DEPTH][2][XI];
 
-  auto load = [&](int buf, int kb) {
+  auto load_step = [&](int slot, int s) {
 #pragma unroll
     for (int t = 0; t < TABLES; ++t)
 #pragma unroll
-      for (int rg = 0; rg < RG; ++rg) {
-        const uint8_t* p = wptr[t][rg] + (size_t)kb * kScaleBlock;
-        wbuf[buf][t][rg][0] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
-        wbuf[buf][t][rg][1] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p + 64));
-        sbuf[buf][t][rg] = sptr[t][rg][kb];
-      }
+      for (int rg = 0; rg < RG; ++rg) load_weight_step(wrows[t][rg], s, lane, wring[slot][t][rg]);
 #pragma unroll
-    for (int cg = 0; cg < CG; ++cg) {
-      if (xok[cg]) {
-        const uint16_t* p = xptr[cg] + (size_t)kb * kScaleBlock;
-        xbuf[buf][cg][0] = *reinterpret_cast<const u32x4*>(p);
-        xbuf[buf][cg][1] = *reinterpret_cast<const u32x4*>(p + 8);
-        xbuf[buf][cg][2] = *reinterpret_cast<const u32x4*>(p + 64);
-        xbuf[buf][cg][3] = *reinterpret_cast<const u32x4*>(p + 72);
-      } else {
-        xbuf[buf][cg][0] = xbuf[buf][cg][1] = xbuf[buf][cg][2] = xbuf[buf][cg][3] =
-            u32x4{0u, 0u, 0u, 0u};
-      }
+    for (int kbl = 0; kbl < 2; ++kbl) {
+      const int kb = 2 * s + kbl;
+#pragma unroll
+      for (int q = 0; q < XI; ++q)
+        xring[slot][kbl][q] = (xok[q] && kb < KB)
+                                  ? *reinterpret_cast<const u32x4*>(xsrc[q] + (size_t)kb * kScaleBlock)
+                                  : u32x4{0u, 0u, 0u, 0u};
     }
   };
 
-  auto compute = [&](int buf) {
+  // stage step s (already in the ring) into LDS, then refill its slot with s + DEPTH
+  auto compute_step = [&](int slot, int s) {
 #pragma unroll
     for (int t = 0; t < TABLES; ++t)
 #pragma unroll
-      for (int rg = 0; rg < RG; ++rg) {
-        const float s = sbuf[buf][t][rg];
-        const u32x4 w0 = wbuf[buf][t][rg][0];
-        const u32x4 w1 = wbuf[buf][t][rg][1];
-        const bf16x8 a0 = decode_fp8x8(w0.x, w0.y, s);
-        const bf16x8 a1 = decode_fp8x8(w0.z, w0.w, s);
-        const bf16x8 a2 = decode_fp8x8(w1.x, w1.y, s);
-        const bf16x8 a3 = decode_fp8x8(w1.z, w1.w, s);
+      for (int rg = 0; rg < RG; ++rg) store_weight_step(region[t * RG + rg], lane, wring[slot][t][rg]);
 #pragma unroll
-        for (int cg = 0; cg < CG; ++cg) {
-          f32x4 c = acc.v[t][rg][cg];
-          c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, as_bf16x8(xbuf[buf][cg][0]), c, 0, 0, 0);
-          c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, as_bf16x8(xbuf[buf][cg][1]), c, 0, 0, 0);
-          c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a2, as_bf16x8(xbuf[buf][cg][2]), c, 0, 0, 0);
-          c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a3, as_bf16x8(xbuf[buf][cg][3]), c, 0, 0, 0);
-          acc.v[t][rg][cg] = c;
+    for (int kbl = 0; kbl < 2; ++kbl)
+#pragma unroll
+      for (int q = 0; q < XI; ++q) store_act_rows(xregion[kbl], q, lane, xring[slot][kbl][q]);
+    __builtin_amdgcn_wave_barrier();
+    if (s + DEPTH < s1) load_step(slot, s + DEPTH);
+#pragma unroll
+    for (int kbl = 0; kbl < 2; ++kbl) {
+      const int kb = 2 * s + kbl;
+      if (kb >= KB) break;
+      bf16x8 B[CG][4];
+#pragma unroll
+      for (int cg = 0; cg < CG; ++cg) {
+        const int i = cg * 16 + lrow;
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          B[cg][j] = i < XROWS ? as_bf16x8(read_act_chunk(xregion[kbl], i, lane, j))
+                               : as_bf16x8(u32x4{0u, 0u, 0u, 0u});
+      }
+#pragma unroll
+      for (int t = 0; t < TABLES; ++t)
+#pragma unroll
+        for (int rg = 0; rg < RG; ++rg) {
+          bf16x8 A[4];
+          decode_weight_block(region[t * RG + rg], lane, kbl, sptr[t][rg][kb], A);
+#pragma unroll
+          for (int cg = 0; cg < CG; ++cg) {
+            f32x4 c = acc[t][rg][cg];
+            c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[0], B[cg][0], c, 0, 0, 0);
+            c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[1], B[cg][1], c, 0, 0, 0);
+            c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[2], B[cg][2], c, 0, 0, 0);
+            c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[3], B[cg][3], c, 0, 0, 0);
+            acc[t][rg][cg] = c;
+          }
         }
-      }
+    }
+    __builtin_amdgcn_wave_barrier();
   };
 
-  if (kb0 < kb1) {
-    load(0, kb0);
-    for (int kb = kb0; kb < kb1; kb += 2) {
-      if (kb + 1 < kb1) load(1, kb + 1);
-      compute(0);
-      if (kb + 1 < kb1) {
-        if (kb + 2 < kb1) load(0, kb + 2);
-        compute(1);
-      }
-    }
+#pragma unroll
+  for (int d = 0; d < DEPTH; ++d)
+    if (s0 + d < s1) load_step(d, s0 + d);
+  for (int s = s0; s < s1; s += DEPTH) {
+#pragma unroll
+    for (int d = 0; d < DEPTH; ++d)
+      if (s + d < s1) compute_step(d, s + d);
   }
 
   // Split-K: waves wk > 0 hand their partial sums to wave wk == 0 through LDS,
@@ -174,7 +198,7 @@ __global__ __launch_bounds__(64 * WN * WK) void grouped_fp8_gemm_kernel(const Gr
         for (int rg = 0; rg < RG; ++rg)
 #pragma unroll
           for (int cg = 0; cg < CG; ++cg)
-            red[wk - 1][wn][(t * RG + rg) * CG + cg][lane] = acc.v[t][rg][cg];
+            red[wk - 1][wn][(t * RG + rg) * CG + cg][lane] = acc[t][rg][cg];
     }
     __syncthreads();
     if (wk > 0) return;
@@ -186,7 +210,7 @@ __global__ __launch_bounds__(64 * WN * WK) void grouped_fp8_gemm_kernel(const Gr
         for (int rg = 0; rg < RG; ++rg)
 #pragma unroll
           for (int cg = 0; cg < CG; ++cg)
-            acc.v[t][rg][cg] += red[w][wn][(t * RG + rg) * CG + cg][lane];
+            acc[t][rg][cg] += red[w][wn][(t * RG + rg) * CG + cg][lane];
   }
 
   // Epilogue: lane holds rows n .. n+3 of route column cg*16 + lrow.
@@ -194,68 +218,34 @@ __global__ __launch_bounds__(64 * WN * WK) void grouped_fp8_gemm_kernel(const Gr
   for (int cg = 0; cg < CG; ++cg) {
     const int col = cg * 16 + lrow;
     if (col >= live) continue;
-    const int r = r0 + col;
-    const int64_t orow = a.out_row_ids ? a.out_row_ids[r] : r;
-    if (orow < 0 || orow >= a.out_rows) continue;
 #pragma unroll
-    for (int rg = 0; rg < RG; ++rg) {
-      const int n = n0 + rg * 16 + lgrp * 4;
-      if constexpr (EPI == kEpiSwiglu) {
-        const f32x4 g = acc.v[0][rg][cg];
-        const f32x4 u = acc.v[TABLES - 1][rg][cg];
-        float v[4];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) v[j] = swiglu_bf16(round_to_bf16(g[j]), round_to_bf16(u[j]));
-        u32x2 pk{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
-        *reinterpret_cast<u32x2*>(static_cast<uint16_t*>(a.out) + orow * a.ldo + n) = pk;
-      } else if constexpr (EPI == kEpiWeighted) {
-        const float wgt = round_to_bf16(a.route_w[orow]);
-        const f32x4 d = acc.v[0][rg][cg];
-        float v[4];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) v[j] = round_to_bf16(d[j]) * wgt;
-        u32x2 pk{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
-        *reinterpret_cast<u32x2*>(static_cast<uint16_t*>(a.out) + orow * a.ldo + n) = pk;
-      } else if constexpr (EPI == kEpiStoreF32) {
-#pragma unroll
-        for (int t = 0; t < TABLES; ++t) {
-          const f32x4 d = acc.v[t][rg][cg];
-          *reinterpret_cast<float4*>(static_cast<float*>(a.out) + orow * a.ldo + t * a.table_stride + n) =
-              float4{d[0], d[1], d[2], d[3]};
-        }
-      } else {
-#pragma unroll
-        for (int t = 0; t < TABLES; ++t) {
-          const f32x4 d = acc.v[t][rg][cg];
-          u32x2 pk{pack_bf16x2(d[0], d[1]), pack_bf16x2(d[2], d[3])};
-          *reinterpret_cast<u32x2*>(static_cast<uint16_t*>(a.out) + orow * a.ldo + t * a.table_stride + n) = pk;
-        }
-      }
-    }
+    for (int rg = 0; rg < RG; ++rg)
+      store_fragment<TABLES, EPI>(a, r0 + col, n0 + rg * 16 + lgrp * 4, acc[0][rg][cg],
+                                  acc[TABLES - 1][rg][cg]);
   }
 }
 
-template <int TABLES, int RG, int CG, int WN, int WK>
+template <int TABLES, int RG, int XROWS, int WN, int WK, int DEPTH>
 hipError_t launch_shape(const GroupedGemmArgs& a, int epilogue, hipStream_t stream) {
   constexpr int BN = WN * RG * 16;
   const dim3 grid(a.max_tiles, a.n / BN);
   const dim3 block(64 * WN * WK);
   switch (epilogue) {
     case kEpiStoreF32:
-      hipLaunchKernelGGL((grouped_fp8_gemm_kernel<TABLES, RG, CG, WN, WK, kEpiStoreF32>), grid, block, 0, stream, a);
+      hipLaunchKernelGGL((grouped_fp8_gemm_kernel<TABLES, RG, XROWS, WN, WK, DEPTH, kEpiStoreF32>), grid, block, 0, stream, a);
       break;
     case kEpiStoreBf16:
-      hipLaunchKernelGGL((grouped_fp8_gemm_kernel<TABLES, RG, CG, WN, WK, kEpiStoreBf16>), grid, block, 0, stream, a);
+      hipLaunchKernelGGL((grouped_fp8_gemm_kernel<TABLES, RG, XROWS, WN, WK, DEPTH, kEpiStoreBf16>), grid, block, 0, stream, a);
       break;
     case kEpiSwiglu:
       if constexpr (TABLES == 2) {
-        hipLaunchKernelGGL((grouped_fp8_gemm_kernel<TABLES, RG, CG, WN, WK, kEpiSwiglu>), grid, block, 0, stream, a);
+        hipLaunchKernelGGL((grouped_fp8_gemm_kernel<TABLES, RG, XROWS, WN, WK, DEPTH, kEpiSwiglu>), grid, block, 0, stream, a);
         break;
       }
       return hipErrorInvalidValue;
     case kEpiWeighted:
       if constexpr (TABLES == 1) {
-        hipLaunchKernelGGL((grouped_fp8_gemm_kernel<TABLES, RG, CG, WN, WK, kEpiWeighted>), grid, block, 0, stream, a);
+        hipLaunchKernelGGL((grouped_fp8_gemm_kernel<TABLES, RG, XROWS, WN, WK, DEPTH, kEpiWeighted>), grid, block, 0, stream, a);
         break;
       }
       return hipErrorInvalidValue;
@@ -270,9 +260,10 @@ hipError_t launch_shape(const GroupedGemmArgs& a, int epilogue, hipStream_t stre
 // Routes per tile of each shape family.
 int gemm_shape_rows(int shape) {
   switch (shape) {
+    case kShapeDecode: return 4;
     case kShapeSkinny: return 16;
     case kShapePanel32: return 32;
-    case kShapeWide: return 64;
+    case kShapeWide: return 128;
     default: return 0;
   }
 }
@@ -280,9 +271,10 @@ int gemm_shape_rows(int shape) {
 // Weight rows per workgroup (the N stripe) of each shape family.
 int gemm_shape_bn(int shape, int tables) {
   switch (shape) {
+    case kShapeDecode: return tables == 2 ? 16 : 32;
     case kShapeSkinny: return tables == 2 ? 16 : 32;
     case kShapePanel32: return tables == 2 ? 64 : 128;
-    case kShapeWide: return tables == 2 ? 64 : 128;
+    case kShapeWide: return tables == 2 ? 128 : 256;
     default: return 0;
   }
 }
@@ -292,17 +284,19 @@ hipError_t launch_grouped_gemm(const GroupedGemmArgs& a, int shape, int tables, 
   if (a.max_tiles <= 0) return hipSuccess;
   if (tables == 2) {
     switch (shape) {
-      case kShapeSkinny: return launch_shape<2, 1, 1, 1, 4>(a, epilogue, stream);
-      case kShapePanel32: return launch_shape<2, 1, 2, 4, 1>(a, epilogue, stream);
-      case kShapeWide: return launch_shape<2, 1, 4, 4, 1>(a, epilogue, stream);
+      case kShapeDecode: return launch_shape<2, 1, 4, 1, 4, 1>(a, epilogue, stream);
+      case kShapeSkinny: return launch_shape<2, 1, 16, 1, 4, 1>(a, epilogue, stream);
+      case kShapePanel32: return launch_shape<2, 1, 32, 4, 1, 1>(a, epilogue, stream);
+      case kShapeWide: return launch_grouped_gemm_wide(a, 2, epilogue, stream);
       default: return hipErrorInvalidValue;
     }
   }
   if (tables == 1) {
     switch (shape) {
-      case kShapeSkinny: return launch_shape<1, 2, 1, 1, 4>(a, epilogue, stream);
-      case kShapePanel32: return launch_shape<1, 2, 2, 4, 1>(a, epilogue, stream);
-      case kShapeWide: return launch_shape<1, 2, 4, 4, 1>(a, epilogue, stream);
+      case kShapeDecode: return launch_shape<1, 1, 4, 2, 2, 1>(a, epilogue, stream);
+      case kShapeSkinny: return launch_shape<1, 1, 16, 2, 2, 1>(a, epilogue, stream);
+      case kShapePanel32: return launch_shape<1, 2, 32, 4, 1, 1>(a, epilogue, stream);
+      case kShapeWide: return launch_grouped_gemm_wide(a, 1, epilogue, stream);
       default: return hipErrorInvalidValue;
     }
   }

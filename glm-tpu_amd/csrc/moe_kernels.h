@@ -93,14 +93,45 @@ struct GroupedGemmArgs {
 
 // Kernel shape families chosen by the host from the number of routes per tile.
 enum GemmShape : int {
-  kShapeSkinny = 0,  // <= 16 routes per tile, split-K over 4 waves (decode)
+  kShapeSkinny = 0,  // <= 16 routes per tile, split-K waves
   kShapePanel32 = 1, // <= 32 routes per tile (reference M32 panels)
-  kShapeWide = 2,    // <= 64 routes per tile (prefill)
+  kShapeWide = 2,    // <= 128 routes per tile, LDS-staged activations (prefill)
+  kShapeDecode = 3,  // <= 4 routes per tile, split-K waves (decode)
 };
 int gemm_shape_rows(int shape);
 int gemm_shape_bn(int shape, int tables);
+hipError_t launch_grouped_gemm_wide(const GroupedGemmArgs& a, int tables, int epilogue, hipStream_t stream);
 hipError_t launch_grouped_gemm(const GroupedGemmArgs& a, int shape, int tables, int epilogue,
                                hipStream_t stream);
+
+// ------------------------------------------------------------------ decode path (<= 64 routes)
+constexpr int kMaxDecodeRoutes = 64;
+
+struct DecodeArgs {
+  const int32_t* ids;          // [routes] flat route expert ids
+  const float* weights;        // [routes] route weights
+  int32_t routes;              // tokens * top_k, <= kMaxDecodeRoutes
+  int32_t top_k;
+  int32_t experts;
+  int32_t key_bits;
+  int32_t drop_unowned;        // out-of-range ids contribute nothing (else: expert 0)
+  int32_t check_weights;       // health also requires finite, non-negative weights
+  int32_t bf16_sum;            // bf16 running route sum (else FP32, one rounding)
+  const uint16_t* hidden_in;   // [tokens, hidden] bf16
+  int32_t hidden;
+  int32_t intermediate;
+  const uint8_t* gate_bits;
+  const float* gate_scale;
+  const uint8_t* up_bits;
+  const float* up_scale;
+  const uint8_t* down_bits;
+  const float* down_scale;
+  uint16_t* act;               // workspace [routes, intermediate] bf16, flat route order
+  uint16_t* out;               // [tokens, hidden] bf16
+  uint8_t* valid;
+  void* between_event;         // nullable hipEvent_t recorded between the two kernels
+};
+hipError_t launch_decode_routed(const DecodeArgs& a, hipStream_t stream);
 
 // ------------------------------------------------------------------ auxiliary
 hipError_t launch_decode_fp8_table(const uint8_t* bits, const float* scale, int64_t n, int64_t k,
