@@ -138,15 +138,14 @@ int routed_experts_impl(const uint16_t* hidden, int64_t tokens, int64_t hidden_s
   int st = record(events, 0, stream);
   if (st) return st;
 
-  if (n <= kMaxDecodeRoutes) {
-    // decode: two kernels that group the routes themselves and fuse the combine
+  if (n <= kMaxDecodeRoutes && decode_path_fits(hidden_size, intermediate)) {
+    // decode: two kernels that find their routes themselves and fuse the combine
     DecodeArgs d{};
     d.ids = route_indices;
     d.weights = route_weights;
     d.routes = (int32_t)n;
     d.top_k = top_k;
     d.experts = num_experts;
-    d.key_bits = key_bits_for(num_experts);
     d.drop_unowned = (flags & GLM_MOE_DROP_UNOWNED) ? 1 : 0;
     d.check_weights = (flags & GLM_MOE_CHECK_WEIGHTS) ? 1 : 0;
     d.bf16_sum = (flags & GLM_MOE_ROUTE_SUM_BF16) ? 1 : 0;

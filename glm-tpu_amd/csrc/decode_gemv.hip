@@ -1,26 +1,33 @@
 // Decode path of the routed experts (at most 64 routes, e.g. T <= 8 tokens x
 // top-8): two kernels, no separate route plan and no separate combine.
 //
-// 1. gate/up: workgroup = (tile j, 16 intermediate rows); WK waves split K.
-// 2. down:    workgroup = 16 hidden rows x every tile; its waves take tiles in
-//    turn, write each route's weighted bf16 result to LDS, and the workgroup
-//    then sums every token's slots in slot order (the route combine of
-//    glm_tpu/layers/moe/routed_experts.py:104-117 / :291-293).
+// 1. gate/up: workgroup = (route j, 16 intermediate rows); WK waves split K.
+// 2. down:    workgroup = 16 hidden rows x every route; its waves take routes
+//    in turn, write each route's weighted bf16 result to LDS, and the
+//    workgroup then sums every token's slots in slot order (the route combine
+//    of glm_tpu/layers/moe/routed_experts.py:104-117 / :291-293).
 //
-// Route grouping happens inside every wave (decode_tile): the <= 64 route ids
-// are matched with one ballot per key bit; each distinct expert (in order of
-// its first route) forms tiles of up to R of its routes.  Every route is
-// computed by exactly one tile, so the order of tiles changes no result.
+// Every active route is computed by exactly one wave; the j-th active route
+// (flat order t * top_k + slot) is found with one ballot.  Routes with an id
+// outside [0, experts) are skipped (drop_unowned) or use expert 0, the
+// reference's safe id.
 //
-// Projections are GEMVs on the vector ALU.  A wave owns 16 weight rows; each
-// 128-bit load instruction covers 4 rows x 256 contiguous bytes (lane l: row
-// 4q + l/16, bytes (l%16)*16), the access pattern that streams HBM at full
-// rate.  Every e4m3 byte is decoded once, bf16(f32(e4m3) * block scale)
+// Projections are GEMVs on the vector ALU.  A wave owns 16 weight rows and a
+// range of K "steps" of 256.  Each 128-bit load instruction covers 4 rows x
+// 256 contiguous bytes (lane l: row 4q + l/16, bytes (l%16)*16), the access
+// pattern that streams HBM at full rate; weight loads are the only vector
+// memory traffic of the stream:
+//   * the 128x128 block scales of the wave's K range are loaded once, one per
+//     lane, and picked per step with v_readlane (the step is wave-uniform);
+//   * the route's activations for the wave's K range are staged once into the
+//     wave's own LDS region (their loads are issued before the first weight
+//     loads, so waiting for them never waits for weights), followed by 16 zero
+//     bf16 that the masked lanes of a half step read.
+// Every e4m3 byte is decoded once, bf16(f32(e4m3) * block scale)
 // (glm_tpu/layers/fp8.py:113-126), and multiplied with the bf16 activations
 // by v_dot2c_f32_bf16 (exact bf16 products, FP32 accumulation).  The 16 lanes
-// that share a row add their partial sums at the end.  Two steps of weights
-// and activations are kept in flight per wave; every load of a step is issued
-// unconditionally, so waiting for a step never drains later ones.
+// that share a row add their partial sums at the end.  DEPTH steps of weights
+// are kept in flight per wave.
 #include "moe_common.h"
 #include "moe_kernels.h"
 
@@ -30,206 +37,240 @@ namespace {
 
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 
-constexpr int kGemvRows = 16;  // weight rows per wave
+constexpr int kGemvRows = 16;      // weight rows per wave
+constexpr int kStepK = 256;        // K per step: 16 lanes x 16 e4m3 bytes
+constexpr int kMaxWaveSteps = 8;   // K range of one wave: 2048 (LDS staging, lane-held scales)
+constexpr int kGateUpWaves = 4;
+constexpr int kDownWaves = 8;
+constexpr int kGateUpDepth = 2;    // two tables: 2 x 32 VGPRs in flight
+constexpr int kDownDepth = 3;      // one table: 3 x 16 VGPRs in flight
+
+constexpr int kNonTemporal = 2;            // buffer load cache policy: streamed once (nt)
+constexpr int kBufferFormat = 0x00020000;  // raw buffer descriptor word 3: 32-bit data format
 
 __device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
+
+// Buffer descriptor over `bytes` bytes from base (out-of-range loads return 0).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rows_buffer(const uint8_t* base, int64_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(base), (short)0, (int)bytes, kBufferFormat);
+}
 
 // Two packed bf16 of a 32-bit word.  The word is taken by value: hipcc 7.2
 // lowers __builtin_bit_cast applied directly to a vector element (v[h]) to a
 // read of element 0 whatever h is.
 __device__ __forceinline__ bf16x2 as_bf16x2(uint32_t v) { return __builtin_bit_cast(bf16x2, v); }
 
-template <int R>
-struct DecodeTile {
+// v's value in lane `src` (wave-uniform index), as a scalar
+__device__ __forceinline__ float lane_value(float v, int src) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), src));
+}
+
+struct DecodeRoute {
   int expert;
-  int count;        // routes in the tile (1..R)
-  int route[R];     // flat route ids t * top_k + slot (route[0] repeated past count)
+  int route;   // flat route id t * top_k + slot
 };
 
-// The j-th tile of the route set, wave-uniform.  Routes with an id outside
-// [0, experts) are skipped (drop_unowned) or take expert 0 (the reference's
-// safe id).  Returns false when j >= tile count.
-template <int R>
-__device__ bool decode_tile(const int32_t* ids, int n, int experts, int key_bits, bool drop_unowned, int j,
-                            DecodeTile<R>& t) {
+// The j-th active route, wave-uniform; false when there are at most j.
+__device__ __forceinline__ bool decode_route(const int32_t* ids, int n, int experts, bool drop_unowned, int j,
+                                             DecodeRoute& r) {
   const int lane = threadIdx.x & 63;
   const int raw = lane < n ? ids[lane] : -1;
   const bool owned = raw >= 0 && raw < experts;
   const int key = lane < n ? (owned ? raw : (drop_unowned ? -1 : 0)) : -1;
-  const bool act = key >= 0;
-  uint64_t peers = __ballot(act);
-  for (int b = 0; b < key_bits; ++b) {
-    const bool bit = act && ((key >> b) & 1);
-    const uint64_t m = __ballot(bit);
-    peers &= bit ? m : ~m;
-  }
-  if (!act) peers = 0;
-  const uint64_t lt = lane == 0 ? 0ull : (~0ull >> (64 - lane));
-  const bool leader = act && (peers & lt) == 0;
-  const int cnt = __popcll(peers);
-  const int ntiles = leader ? (cnt + R - 1) / R : 0;
-  int incl = ntiles;
-#pragma unroll
-  for (int d = 1; d < 64; d <<= 1) {
-    const int v = __shfl_up(incl, d, 64);
-    if (lane >= d) incl += v;
-  }
-  const int excl = incl - ntiles;
-  const int total = uniform(__shfl(incl, 63, 64));
-  if (j >= total) return false;
-  const uint64_t hit = __ballot(leader && j >= excl && j < incl);
-  const int src = uniform(__ffsll((unsigned long long)hit) - 1);
-  const int chunk = j - uniform(__shfl(excl, src, 64));
-  t.expert = uniform(__shfl(key, src, 64));
-  const uint32_t lo = uniform(__shfl((int)(uint32_t)peers, src, 64));
-  const uint32_t hi = uniform(__shfl((int)(uint32_t)(peers >> 32), src, 64));
-  uint64_t members = ((uint64_t)hi << 32) | lo;
-  for (int skip = 0; skip < chunk * R; ++skip) members &= members - 1;
-  t.count = 0;
-  int first = 0;
-#pragma unroll
-  for (int r = 0; r < R; ++r) {
-    if (members != 0) {
-      t.route[r] = __ffsll((unsigned long long)members) - 1;
-      members &= members - 1;
-      t.count = r + 1;
-      if (r == 0) first = t.route[0];
-    } else {
-      t.route[r] = first;
-    }
-  }
+  uint64_t active = __ballot(key >= 0);
+  if (__popcll(active) <= j) return false;
+  for (int skip = 0; skip < j; ++skip) active &= active - 1;
+  r.route = uniform(__ffsll((unsigned long long)active) - 1);
+  r.expert = uniform(__shfl(key, r.route, 64));
   return true;
 }
 
-// One step of one wave: 16 rows x 256 K of TABLES tables, and R routes' activations.
-template <int TABLES, int R>
-struct GemvSlot {
-  u32x4 w[TABLES][4];   // rows 4q + lane/16, 16 bytes at lane%16
-  u32x4 x[R][2];        // 16 bf16 activations per route at the same K
-  float s_lo[TABLES];   // scales of the step's two K blocks (wave-uniform)
-  float s_hi[TABLES];
-  bool keep;            // false for the masked lanes of a half step
-};
-
-template <int TABLES, int R>
+// The K range [step_begin, step_end) of one wave over TABLES tables of the
+// same 16 rows, against one route's activations.
+template <int TABLES>
 struct GemvStream {
-  const uint8_t* wrow[TABLES];  // start of the lane's first row (row0 + lane/16)
-  const float* srow[TABLES];    // scale row of the 16 rows (K/128 entries)
-  const uint16_t* xrow[R];
-  int64_t row_stride;
+  __amdgpu_buffer_rsrc_t w[TABLES];  // the 16 rows of each table (descriptor in SGPRs)
+  uint32_t lane_off;            // (lane/16) * row_stride + (lane%16) * 16
+  float sreg[TABLES];           // lane l: block scale 2 * step_begin + l of the rows
+  int64_t row_stride;           // bytes between weight rows (= k)
   int k;
+  int kblocks;                  // k / 128
+  int step_begin, step_end;
+  const uint16_t* x;            // global activation row (bf16, k entries)
+  uint16_t* xs;                 // the wave's LDS region: K range, then 16 zero bf16
+  int pad;                      // element offset of the zeros in xs
 };
 
-template <int TABLES, int R>
-__device__ __forceinline__ void gemv_load(const GemvStream<TABLES, R>& g, int step, int lane,
-                                          GemvSlot<TABLES, R>& sl) {
-  const int kofs = step * 256 + (lane & 15) * 16;
-  // a half step (the last one of an odd K/128) masks its upper eight lanes;
-  // their loads read in-bounds bytes that are then multiplied by zero
-  sl.keep = kofs < g.k;
-  const int kk = sl.keep ? kofs : g.k - 16;
-  const int kb_hi = min(2 * step + 1, (g.k >> 7) - 1);
+// Activations of the wave's K range into registers (at most 4 x 16 bytes a lane).
+template <int TABLES>
+__device__ __forceinline__ void stage_x_load(const GemvStream<TABLES>& g, int lane, u32x4 (&xv)[4]) {
+  const int kbeg = g.step_begin * kStepK;
+  const int chunks = (min(g.step_end * kStepK, g.k) - kbeg) >> 3;
 #pragma unroll
-  for (int t = 0; t < TABLES; ++t) {
+  for (int i = 0; i < 4; ++i) {
+    const int c = lane + 64 * i;
+    if (c < chunks) xv[i] = *reinterpret_cast<const u32x4*>(g.x + kbeg + 8 * c);
+  }
+}
+
+template <int TABLES>
+__device__ __forceinline__ void stage_x_store(const GemvStream<TABLES>& g, int lane, const u32x4 (&xv)[4]) {
+  const int kbeg = g.step_begin * kStepK;
+  const int chunks = (min(g.step_end * kStepK, g.k) - kbeg) >> 3;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int c = lane + 64 * i;
+    if (c < chunks) *reinterpret_cast<u32x4*>(g.xs + 8 * c) = xv[i];
+  }
+  if (lane < 2) *reinterpret_cast<u32x4*>(g.xs + g.pad + 8 * lane) = u32x4{0u, 0u, 0u, 0u};
+}
+
+// Weights of step s0 + s: rows 4q + lane/16, 16 bytes at K = (s0 + s) * 256 + (lane%16) * 16.
+// FULL: every step of the range is whole.  Otherwise the masked lanes of a
+// half step (the last step of an odd k/128) load the row's last 16 bytes, in
+// bounds; their products are zero.
+template <bool FULL, int TABLES>
+__device__ __forceinline__ void gemv_load(const GemvStream<TABLES>& g, int s, int lane, u32x4 (&w)[TABLES][4]) {
+  // buffer loads: lane offset (VGPR) + step (immediate) + row group and range start (SGPR)
+  uint32_t off = g.lane_off + s * kStepK;
+  if constexpr (!FULL) {
+    const int kofs = (g.step_begin + s) * kStepK + (lane & 15) * 16;
+    if (kofs >= g.k) off -= (uint32_t)(kofs - (g.k - 16));
+  }
+#pragma unroll
+  for (int t = 0; t < TABLES; ++t)
 #pragma unroll
     for (int q = 0; q < 4; ++q)
-      sl.w[t][q] = __builtin_nontemporal_load(
-          reinterpret_cast<const u32x4*>(g.wrow[t] + (int64_t)(4 * q) * g.row_stride + kk));
-    sl.s_lo[t] = g.srow[t][2 * step];
-    sl.s_hi[t] = g.srow[t][kb_hi];
-  }
-#pragma unroll
-  for (int r = 0; r < R; ++r) {
-    const u32x4* p = reinterpret_cast<const u32x4*>(g.xrow[r] + kk);
-    sl.x[r][0] = p[0];
-    sl.x[r][1] = p[1];
-  }
+      w[t][q] = __builtin_bit_cast(
+          u32x4, __builtin_amdgcn_raw_buffer_load_b128(g.w[t], off, 4 * q * (int)g.row_stride + g.step_begin * kStepK,
+                                                       kNonTemporal));
 }
 
-// acc[t][q][r] += sum over the lane's 16 K of bf16(e4m3 * scale) * x
-template <int TABLES, int R>
-__device__ __forceinline__ void gemv_fma(const GemvSlot<TABLES, R>& sl, int nr, int lane,
-                                         float (&acc)[TABLES][4][R]) {
+// acc[t][q] += sum over the lane's 16 K of bf16(e4m3 * scale) * x, for step s0 + s
+template <bool FULL, int TABLES>
+__device__ __forceinline__ void gemv_fma(const GemvStream<TABLES>& g, const u32x4 (&w)[TABLES][4], int s,
+                                         int lane, float (&acc)[TABLES][4]) {
+  int xoff = s * kStepK + (lane & 15) * 16;
+  int b_hi = 2 * s + 1;
+  bool keep = true;
+  if constexpr (!FULL) {
+    keep = (g.step_begin + s) * kStepK + (lane & 15) * 16 < g.k;
+    xoff = keep ? xoff : g.pad;
+    b_hi = min(2 * (g.step_begin + s) + 1, g.kblocks - 1) - 2 * g.step_begin;
+  }
+  const u32x4 x0 = *reinterpret_cast<const u32x4*>(g.xs + xoff);
+  const u32x4 x1 = *reinterpret_cast<const u32x4*>(g.xs + xoff + 8);
 #pragma unroll
   for (int t = 0; t < TABLES; ++t) {
-    const float scale = sl.keep ? ((lane & 15) < 8 ? sl.s_lo[t] : sl.s_hi[t]) : 0.0f;
+    const float s_lo = lane_value(g.sreg[t], 2 * s);
+    const float s_hi = lane_value(g.sreg[t], b_hi);
+    float scale = (lane & 15) < 8 ? s_lo : s_hi;
+    if constexpr (!FULL) scale = keep ? scale : 0.0f;
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-      const u32x4 w = sl.w[t][q];
-      const u32x4 lo = __builtin_bit_cast(u32x4, decode_fp8x8(w[0], w[1], scale));
-      const u32x4 hi = __builtin_bit_cast(u32x4, decode_fp8x8(w[2], w[3], scale));
+      const u32x4 lo = __builtin_bit_cast(u32x4, decode_fp8x8(w[t][q][0], w[t][q][1], scale));
+      const u32x4 hi = __builtin_bit_cast(u32x4, decode_fp8x8(w[t][q][2], w[t][q][3], scale));
+      float a = acc[t][q];
 #pragma unroll
-      for (int r = 0; r < R; ++r) {
-        if (r < nr) {
-          float a = acc[t][q][r];
-#pragma unroll
-          for (int h = 0; h < 4; ++h) {
-            const uint32_t wv = lo[h], xv = sl.x[r][0][h];
-            a = __builtin_amdgcn_fdot2_f32_bf16(as_bf16x2(wv), as_bf16x2(xv), a, false);
-          }
-#pragma unroll
-          for (int h = 0; h < 4; ++h) {
-            const uint32_t wv = hi[h], xv = sl.x[r][1][h];
-            a = __builtin_amdgcn_fdot2_f32_bf16(as_bf16x2(wv), as_bf16x2(xv), a, false);
-          }
-          acc[t][q][r] = a;
-        }
+      for (int h = 0; h < 4; ++h) {
+        const uint32_t wv = lo[h], xv = x0[h];
+        a = __builtin_amdgcn_fdot2_f32_bf16(as_bf16x2(wv), as_bf16x2(xv), a, false);
       }
+#pragma unroll
+      for (int h = 0; h < 4; ++h) {
+        const uint32_t wv = hi[h], xv = x1[h];
+        a = __builtin_amdgcn_fdot2_f32_bf16(as_bf16x2(wv), as_bf16x2(xv), a, false);
+      }
+      acc[t][q] = a;
     }
   }
 }
 
-// Straight-line stream of exactly NSTEPS steps from s0, two steps in flight:
-// with no loop back-edge the compiler counts outstanding loads exactly and
-// waits only for the step it is about to multiply.
-template <int NSTEPS, int TABLES, int R>
-__device__ __forceinline__ void gemv_run_fixed(const GemvStream<TABLES, R>& g, int s0, int nr, int lane,
-                                               float (&acc)[TABLES][4][R]) {
-  GemvSlot<TABLES, R> ring[2];
-  gemv_load(g, s0, lane, ring[0]);
-  if constexpr (NSTEPS > 1) gemv_load(g, s0 + 1, lane, ring[1]);
+// Straight-line stream of exactly NSTEPS steps, DEPTH in flight: with no loop
+// back-edge the compiler counts outstanding loads exactly and waits only for
+// the step it is about to multiply.  Order of issue: activation staging
+// loads, the first DEPTH weight steps, then the staging stores (which wait
+// for the activations only).
+template <int NSTEPS, int DEPTH, int TABLES>
+__device__ __forceinline__ void gemv_run_fixed(const GemvStream<TABLES>& g, int lane, float (&acc)[TABLES][4]) {
+  constexpr int D = DEPTH < NSTEPS ? DEPTH : NSTEPS;
+  u32x4 xv[4];
+  stage_x_load(g, lane, xv);
+  __builtin_amdgcn_sched_barrier(0);
+  u32x4 ring[D][TABLES][4];
+#pragma unroll
+  for (int d = 0; d < D; ++d) {
+    gemv_load<true>(g, d, lane, ring[d]);
+    __builtin_amdgcn_sched_barrier(0);  // issue step by step: waiting for one never waits for the next
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  stage_x_store(g, lane, xv);
+  __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
   for (int s = 0; s < NSTEPS; ++s) {
-    gemv_fma(ring[s & 1], nr, lane, acc);
-    if (s + 2 < NSTEPS) {
+    gemv_fma<true>(g, ring[s % D], s, lane, acc);
+    if (s + D < NSTEPS) {
       __builtin_amdgcn_sched_barrier(0);
-      gemv_load(g, s0 + s + 2, lane, ring[s & 1]);
+      gemv_load<true>(g, s + D, lane, ring[s % D]);
     }
   }
 }
 
-// Stream steps [s0, s1) of the 16 rows, two steps in flight.  The usual step
-// counts run straight-line; others use a loop whose refills are issued
-// unconditionally (a refill past the end reloads the last step, an L2 hit).
-template <int TABLES, int R>
-__device__ __forceinline__ void gemv_run(const GemvStream<TABLES, R>& g, int s0, int s1, int nr, int lane,
-                                         float (&acc)[TABLES][4][R]) {
-  if (s0 >= s1) return;
-  switch (s1 - s0) {
-    case 1: gemv_run_fixed<1>(g, s0, nr, lane, acc); return;
-    case 2: gemv_run_fixed<2>(g, s0, nr, lane, acc); return;
-    case 3: gemv_run_fixed<3>(g, s0, nr, lane, acc); return;
-    case 4: gemv_run_fixed<4>(g, s0, nr, lane, acc); return;
-    case 6: gemv_run_fixed<6>(g, s0, nr, lane, acc); return;
-    case 8: gemv_run_fixed<8>(g, s0, nr, lane, acc); return;
-    case 12: gemv_run_fixed<12>(g, s0, nr, lane, acc); return;
-    default: break;
-  }
-  const int last = s1 - 1;
-  GemvSlot<TABLES, R> ring[2];
-  gemv_load(g, s0, lane, ring[0]);
-  gemv_load(g, min(s0 + 1, last), lane, ring[1]);
-  // The scheduling barriers keep each refill after the multiplications that
-  // consume its slot, so a slot's registers are reused in place (no copies of
-  // in-flight registers at the loop back-edge, which would force full waits).
-  for (int s = s0; s < s1; s += 2) {
-    gemv_fma(ring[0], nr, lane, acc);
+// Any range, half step included: a loop over groups of DEPTH steps whose
+// refills are issued unconditionally (a refill past the end reloads the last step).
+template <int DEPTH, int TABLES>
+__device__ __forceinline__ void gemv_run_loop(const GemvStream<TABLES>& g, int lane, float (&acc)[TABLES][4]) {
+  const int n = g.step_end - g.step_begin, last = n - 1;
+  u32x4 xv[4];
+  stage_x_load(g, lane, xv);
+  __builtin_amdgcn_sched_barrier(0);
+  u32x4 ring[DEPTH][TABLES][4];
+#pragma unroll
+  for (int d = 0; d < DEPTH; ++d) {
+    gemv_load<false>(g, min(d, last), lane, ring[d]);
     __builtin_amdgcn_sched_barrier(0);
-    gemv_load(g, min(s + 2, last), lane, ring[0]);
-    if (s + 1 < s1) gemv_fma(ring[1], nr, lane, acc);
-    __builtin_amdgcn_sched_barrier(0);
-    gemv_load(g, min(s + 3, last), lane, ring[1]);
   }
+  __builtin_amdgcn_sched_barrier(0);
+  stage_x_store(g, lane, xv);
+  __builtin_amdgcn_sched_barrier(0);
+  for (int s = 0; s < n; s += DEPTH) {
+#pragma unroll
+    for (int d = 0; d < DEPTH; ++d) {
+      if (s + d < n) gemv_fma<false>(g, ring[d], s + d, lane, acc);
+      __builtin_amdgcn_sched_barrier(0);
+      gemv_load<false>(g, min(s + d + DEPTH, last), lane, ring[d]);
+    }
+  }
+}
+
+template <int DEPTH, int TABLES>
+__device__ __forceinline__ void gemv_run(const GemvStream<TABLES>& g, int lane, float (&acc)[TABLES][4]) {
+  const int n = g.step_end - g.step_begin;
+  if (n <= 0) return;
+  // a half step exists when k / 128 is odd; it is the last step of the last range
+  const bool half = (g.kblocks & 1) && g.step_end * kStepK > g.k;
+  if (!half) {
+    switch (n) {
+      case 2: gemv_run_fixed<2, DEPTH>(g, lane, acc); return;
+      case 4: gemv_run_fixed<4, DEPTH>(g, lane, acc); return;
+      case 6: gemv_run_fixed<6, DEPTH>(g, lane, acc); return;
+      case 8:
+        // two tables: eight straight-line steps exceed the register budget
+        if constexpr (TABLES == 1) {
+          gemv_run_fixed<8, DEPTH>(g, lane, acc);
+          return;
+        }
+        break;
+      default: break;
+    }
+  }
+  gemv_run_loop<DEPTH>(g, lane, acc);
+}
+
+// Block scales 2 * step_begin + lane of the 16 rows (rows share one 128-row block).
+__device__ __forceinline__ float lane_scale(const float* srow, int kblocks, int step_begin, int lane) {
+  const int b = 2 * step_begin + lane;
+  return b < kblocks ? srow[b] : 0.0f;
 }
 
 // Sum over the 16 lanes that share rows; every lane of the group gets the sum.
@@ -241,92 +282,103 @@ __device__ __forceinline__ float sum16(float v) {
   return v;
 }
 
+__host__ __device__ constexpr int xs_elems(int wave_steps) { return wave_steps * kStepK + 16; }
+
 // ------------------------------------------------------------------ gate/up + SwiGLU
-template <int R, int WK>
-__global__ __launch_bounds__(64 * WK) void decode_gate_up_kernel(const DecodeArgs a) {
-  __shared__ float red[WK][2][kGemvRows][R];
+template <int WK>
+__global__ __launch_bounds__(64 * WK) __attribute__((amdgpu_waves_per_eu(4)))
+void decode_gate_up_kernel(const DecodeArgs a, int wave_steps) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  float(*red)[2][kGemvRows] = reinterpret_cast<float(*)[2][kGemvRows]>(smem);
   const int lane = threadIdx.x & 63;
   const int wk = uniform(threadIdx.x >> 6);  // wave-uniform: scalar loop control
-  DecodeTile<R> tile;
-  if (!decode_tile<R>(a.ids, a.routes, a.experts, a.key_bits, a.drop_unowned, blockIdx.x, tile)) return;
+  DecodeRoute rt;
+  if (!decode_route(a.ids, a.routes, a.experts, a.drop_unowned, blockIdx.x, rt)) return;
   const int I = a.intermediate, H = a.hidden;
   const int row0 = blockIdx.y * kGemvRows;
-  GemvStream<2, R> g;
+  const int steps = (H + kStepK - 1) / kStepK;
+  GemvStream<2> g;
+  g.k = H;
+  g.kblocks = H / kScaleBlock;
+  g.row_stride = H;
+  g.lane_off = (uint32_t)((lane >> 4) * H + (lane & 15) * 16);
+  g.step_begin = min(wk * wave_steps, steps);
+  g.step_end = min(g.step_begin + wave_steps, steps);
   const uint8_t* tables[2] = {a.gate_bits, a.up_bits};
   const float* scales[2] = {a.gate_scale, a.up_scale};
 #pragma unroll
   for (int t = 0; t < 2; ++t) {
-    g.wrow[t] = tables[t] + ((int64_t)tile.expert * I + row0 + (lane >> 4)) * H;
-    g.srow[t] = scales[t] + ((int64_t)tile.expert * (I / kScaleBlock) + row0 / kScaleBlock) * (H / kScaleBlock);
+    g.w[t] = rows_buffer(tables[t] + ((int64_t)rt.expert * I + row0) * H, (int64_t)kGemvRows * H);
+    const float* srow = scales[t] + ((int64_t)rt.expert * (I / kScaleBlock) + row0 / kScaleBlock) * g.kblocks;
+    g.sreg[t] = lane_scale(srow, g.kblocks, g.step_begin, lane);
   }
-#pragma unroll
-  for (int r = 0; r < R; ++r) g.xrow[r] = a.hidden_in + (int64_t)(tile.route[r] / a.top_k) * H;
-  g.row_stride = H;
-  g.k = H;
-  const int steps = (H / kScaleBlock + 1) / 2;
-  float acc[2][4][R] = {};
-  gemv_run(g, (steps * wk) / WK, (steps * (wk + 1)) / WK, tile.count, lane, acc);
+  g.x = a.hidden_in + (int64_t)(rt.route / a.top_k) * H;
+  g.xs = reinterpret_cast<uint16_t*>(smem + sizeof(float) * WK * 2 * kGemvRows) + wk * xs_elems(wave_steps);
+  g.pad = wave_steps * kStepK;
+  float acc[2][4] = {};
+  gemv_run<kGateUpDepth>(g, lane, acc);
 #pragma unroll
   for (int t = 0; t < 2; ++t)
 #pragma unroll
-    for (int q = 0; q < 4; ++q)
-#pragma unroll
-      for (int r = 0; r < R; ++r) {
-        const float v = sum16(acc[t][q][r]);
-        if ((lane & 15) == 0) red[wk][t][4 * q + (lane >> 4)][r] = v;
-      }
-  __syncthreads();
-  // one thread per (row, route): wave-order split-K sum, then the bf16 SwiGLU
-  const int tid = threadIdx.x;
-  if (tid < kGemvRows * R) {
-    const int row = tid / R, r = tid % R;
-    if (r < tile.count) {
-      float gsum = 0.f, usum = 0.f;
-      for (int w = 0; w < WK; ++w) {
-        gsum += red[w][0][row][r];
-        usum += red[w][1][row][r];
-      }
-      const float v = swiglu_bf16(round_to_bf16(gsum), round_to_bf16(usum));
-      a.act[(int64_t)tile.route[r] * I + row0 + row] = f32_to_bf16_bits(v);
+    for (int q = 0; q < 4; ++q) {
+      const float v = sum16(acc[t][q]);
+      if ((lane & 15) == 0) red[wk][t][4 * q + (lane >> 4)] = v;
     }
+  __syncthreads();
+  // one thread per row: wave-order split-K sum, then the bf16 SwiGLU
+  const int tid = threadIdx.x;
+  if (tid < kGemvRows) {
+    float gsum = 0.f, usum = 0.f;
+    for (int w = 0; w < WK; ++w) {
+      gsum += red[w][0][tid];
+      usum += red[w][1][tid];
+    }
+    const float v = swiglu_bf16(round_to_bf16(gsum), round_to_bf16(usum));
+    a.act[(int64_t)rt.route * I + row0 + tid] = f32_to_bf16_bits(v);
   }
 }
 
 // ------------------------------------------------------------------ down + weighting + combine
-template <int R, int WAVES>
-__global__ __launch_bounds__(64 * WAVES) void decode_down_kernel(const DecodeArgs a) {
-  __shared__ float res[kMaxDecodeRoutes][kGemvRows];
+template <int WAVES>
+__global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(4)))
+void decode_down_kernel(const DecodeArgs a) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  float(*res)[kGemvRows] = reinterpret_cast<float(*)[kGemvRows]>(smem);  // [kMaxDecodeRoutes][16]
   const int lane = threadIdx.x & 63;
   const int wave = uniform(threadIdx.x >> 6);  // wave-uniform: scalar loop control
   const int tid = threadIdx.x;
   const int I = a.intermediate, H = a.hidden;
   const int row0 = blockIdx.x * kGemvRows;
+  const int steps = (I + kStepK - 1) / kStepK;
   for (int i = tid; i < a.routes * kGemvRows; i += 64 * WAVES) res[i / kGemvRows][i % kGemvRows] = 0.f;
   __syncthreads();
-  const int steps = (I / kScaleBlock + 1) / 2;
+  uint16_t* xs = reinterpret_cast<uint16_t*>(smem + sizeof(float) * kMaxDecodeRoutes * kGemvRows) +
+                 wave * xs_elems(steps);
   for (int j = wave;; j += WAVES) {
-    DecodeTile<R> tile;
-    if (!decode_tile<R>(a.ids, a.routes, a.experts, a.key_bits, a.drop_unowned, j, tile)) break;
-    GemvStream<1, R> g;
-    g.wrow[0] = a.down_bits + ((int64_t)tile.expert * H + row0 + (lane >> 4)) * I;
-    g.srow[0] = a.down_scale + ((int64_t)tile.expert * (H / kScaleBlock) + row0 / kScaleBlock) * (I / kScaleBlock);
-#pragma unroll
-    for (int r = 0; r < R; ++r) g.xrow[r] = a.act + (int64_t)tile.route[r] * I;
-    g.row_stride = I;
+    DecodeRoute rt;
+    if (!decode_route(a.ids, a.routes, a.experts, a.drop_unowned, j, rt)) break;
+    GemvStream<1> g;
     g.k = I;
-    float acc[1][4][R] = {};
-    gemv_run(g, 0, steps, tile.count, lane, acc);
+    g.kblocks = I / kScaleBlock;
+    g.row_stride = I;
+    g.step_begin = 0;
+    g.step_end = steps;
+    g.w[0] = rows_buffer(a.down_bits + ((int64_t)rt.expert * H + row0) * I, (int64_t)kGemvRows * I);
+    g.lane_off = (uint32_t)((lane >> 4) * I + (lane & 15) * 16);
+    const float* srow = a.down_scale + ((int64_t)rt.expert * (H / kScaleBlock) + row0 / kScaleBlock) * g.kblocks;
+    g.sreg[0] = lane_scale(srow, g.kblocks, 0, lane);
+    g.x = a.act + (int64_t)rt.route * I;
+    g.xs = xs;
+    g.pad = steps * kStepK;
+    const float wr = round_to_bf16(a.weights[rt.route]);  // loaded before the weight stream
+    float acc[1][4] = {};
+    gemv_run<kDownDepth>(g, lane, acc);
 #pragma unroll
-    for (int q = 0; q < 4; ++q)
-#pragma unroll
-      for (int r = 0; r < R; ++r) {
-        const float v = sum16(acc[0][q][r]);
-        if ((lane & 15) == 0 && r < tile.count) {
-          const int route = tile.route[r];
-          // bf16 down output times the bf16 route weight, rounded (routed_experts.py:104-105)
-          res[route][4 * q + (lane >> 4)] = round_to_bf16(round_to_bf16(v) * round_to_bf16(a.weights[route]));
-        }
-      }
+    for (int q = 0; q < 4; ++q) {
+      const float v = sum16(acc[0][q]);
+      // bf16 down output times the bf16 route weight, rounded (routed_experts.py:104-105)
+      if ((lane & 15) == 0) res[rt.route][4 * q + (lane >> 4)] = round_to_bf16(round_to_bf16(v) * wr);
+    }
   }
   __syncthreads();
   // route combine: every token's slots in slot order, FP32 (or bf16 running) sum
@@ -358,26 +410,41 @@ __global__ __launch_bounds__(64 * WAVES) void decode_down_kernel(const DecodeArg
   }
 }
 
-template <int R>
-hipError_t launch_decode(const DecodeArgs& a, hipStream_t stream) {
+int gate_up_wave_steps(int hidden) {
+  const int steps = (hidden + kStepK - 1) / kStepK;
+  return (steps + kGateUpWaves - 1) / kGateUpWaves;
+}
+
+}  // namespace
+
+bool decode_path_fits(int64_t hidden, int64_t intermediate) {
+  return hidden % kGemvRows == 0 && hidden <= (int64_t)kGateUpWaves * kMaxWaveSteps * kStepK &&
+         intermediate <= (int64_t)kMaxWaveSteps * kStepK;
+}
+
+hipError_t launch_decode_routed(const DecodeArgs& a, hipStream_t stream) {
+  if (a.routes <= 0 || a.routes > kMaxDecodeRoutes || a.top_k <= 0 || a.routes % a.top_k != 0 ||
+      !decode_path_fits(a.hidden, a.intermediate) || a.hidden % kScaleBlock != 0 ||
+      a.intermediate % kScaleBlock != 0)
+    return hipErrorInvalidValue;
+  const int gu_steps = gate_up_wave_steps(a.hidden);
+  const size_t gu_lds = sizeof(float) * kGateUpWaves * 2 * kGemvRows +
+                        sizeof(uint16_t) * kGateUpWaves * xs_elems(gu_steps);
   const dim3 g1(a.routes, a.intermediate / kGemvRows);
-  hipLaunchKernelGGL((decode_gate_up_kernel<R, 4>), g1, dim3(256), 0, stream, a);
+  hipLaunchKernelGGL((decode_gate_up_kernel<kGateUpWaves>), g1, dim3(64 * kGateUpWaves), gu_lds, stream, a,
+                     gu_steps);
   hipError_t err = hipGetLastError();
   if (err != hipSuccess) return err;
   if (a.between_event) {
     err = hipEventRecord(static_cast<hipEvent_t>(a.between_event), stream);
     if (err != hipSuccess) return err;
   }
-  hipLaunchKernelGGL((decode_down_kernel<R, 8>), dim3(a.hidden / kGemvRows), dim3(512), 0, stream, a);
+  const int d_steps = (a.intermediate + kStepK - 1) / kStepK;
+  const size_t d_lds = sizeof(float) * kMaxDecodeRoutes * kGemvRows +
+                       sizeof(uint16_t) * kDownWaves * xs_elems(d_steps);
+  hipLaunchKernelGGL((decode_down_kernel<kDownWaves>), dim3(a.hidden / kGemvRows), dim3(64 * kDownWaves), d_lds,
+                     stream, a);
   return hipGetLastError();
-}
-
-}  // namespace
-
-// One token: every expert carries one route (duplicates split into one-route
-// tiles); more tokens: tiles of up to four routes share each weight byte.
-hipError_t launch_decode_routed(const DecodeArgs& a, hipStream_t stream) {
-  return a.routes <= a.top_k ? launch_decode<1>(a, stream) : launch_decode<4>(a, stream);
 }
 
 }  // namespace glm_moe

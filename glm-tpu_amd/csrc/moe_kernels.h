@@ -113,7 +113,6 @@ struct DecodeArgs {
   int32_t routes;              // tokens * top_k, <= kMaxDecodeRoutes
   int32_t top_k;
   int32_t experts;
-  int32_t key_bits;
   int32_t drop_unowned;        // out-of-range ids contribute nothing (else: expert 0)
   int32_t check_weights;       // health also requires finite, non-negative weights
   int32_t bf16_sum;            // bf16 running route sum (else FP32, one rounding)
@@ -131,6 +130,9 @@ struct DecodeArgs {
   uint8_t* valid;
   void* between_event;         // nullable hipEvent_t recorded between the two kernels
 };
+// The decode kernels stage one wave's K range (<= 2048) in LDS: hidden <= 8192
+// (four waves split it), intermediate <= 2048.
+bool decode_path_fits(int64_t hidden, int64_t intermediate);
 hipError_t launch_decode_routed(const DecodeArgs& a, hipStream_t stream);
 
 // ------------------------------------------------------------------ auxiliary
