@@ -49,7 +49,22 @@ def parse_args():
                    help="comma-separated extra configs measured after the headline ('' for none)")
     p.add_argument("--secondary-steps", type=int, default=20)
     p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--copy-calibration", action="store_true",
+                   help="after the headline, copy a 1 GiB device buffer 3 times (the known-size kernel that "
+                        "scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings)")
     return p.parse_args()
+
+
+def copy_calibration(device, nbytes=1 << 30, times=3):
+    """Device-to-device copies of a known size, for calibrating HBM byte counters."""
+    import torch
+
+    src = torch.ones(nbytes, dtype=torch.uint8, device=device)
+    dst = torch.empty_like(src)
+    for _ in range(times):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    del src, dst
 
 
 class Workload:
@@ -136,6 +151,50 @@ def summarize(work, ms, stages, order):
     }
 
 
+DECODE_PATH_MAX_ROUTES = 64  # routes handled by the two decode GEMV kernels (libglm_moe)
+
+# HBM bytes per launch of the dominant kernel, measured with rocprofv3 --pmc
+# (FETCH_SIZE + WRITE_SIZE per dispatch, FETCH_SIZE x2 and WRITE_SIZE x1 by the
+# 1 GiB copy calibration of `bench.py --copy-calibration`); the command and the
+# raw counter summary are in the named profile.
+MEASURED_TRAFFIC = {
+    ("decode_t1", "decode_gate_up_kernel"): {"bytes": 201.79e6, "source": "profiles/decode_t1_hbm_traffic.md"},
+}
+
+
+def dominant_roofline(cfg, head):
+    """Roofline of the stage that dominates the layer: the gate/up projection.
+
+    Decode shapes (at most 64 routes) run the decode GEMV gate/up kernel and are
+    bounded by HBM: achieved = its algorithmic bytes (the selected experts'
+    gate and up e4m3 bytes and scales, the hidden rows and the activations it
+    writes) / its kernel time.  Larger shapes run the grouped GEMM gate/up
+    kernel: achieved = its algorithmic flops / its kernel time against the bf16
+    MFMA peak.  Kernel times come from HIP events the kernel records at its own
+    start and end on the launch stream.
+    """
+    gate_up_us = head["stage_us"]["gate_up"]
+    decode_path = cfg.tokens * cfg.top_k <= DECODE_PATH_MAX_ROUTES
+    if decode_path:
+        kernel = "decode_gate_up_kernel"
+        achieved = head["gate_up_bytes"] / (gate_up_us * 1e-6) / 1e9
+        line = {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": achieved / HBM_PEAK_GBS}
+    else:
+        kernel = "grouped_fp8_gemm_wide_kernel (gate/up, SwiGLU epilogue)"
+        achieved = head["gate_up_tflops"]
+        line = {"bound": "mfma", "achieved": achieved, "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                "frac": achieved / BF16_PEAK_TFLOPS}
+    measured = MEASURED_TRAFFIC.get((cfg.name, kernel))
+    line["traffic"] = measured["bytes"] if measured else None
+    line["kernel"] = kernel
+    line["kernel_us"] = gate_up_us
+    line["algorithmic_bytes"] = head["gate_up_bytes"]
+    if measured:
+        line["traffic_source"] = measured["source"]
+    return line
+
+
 def cpu_baseline(work, device):
     """The numpy oracle on this host's cores, on one layer of the same workload."""
     import torch
@@ -202,16 +261,9 @@ def main():
     head = summarize(work, ms, stages, order)
     head["us_per_layer_with_stage_events"] = ms_ev * 1e3
 
-    decode_like = cfg.tokens * cfg.top_k <= 8 * cfg.experts
-    if decode_like:
-        achieved = head["gate_up_bytes"] / (head["stage_us"]["gate_up"] * 1e-6) / 1e9
-        roofline = {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                    "frac": achieved / HBM_PEAK_GBS, "traffic": None, "kernel": "grouped_fp8_gemm gate/up+SwiGLU"}
-    else:
-        achieved = head["gate_up_tflops"]
-        roofline = {"bound": "mfma", "achieved": achieved, "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
-                    "frac": achieved / BF16_PEAK_TFLOPS, "traffic": None,
-                    "kernel": "grouped_fp8_gemm gate/up+SwiGLU"}
+    roofline = dominant_roofline(cfg, head)
+    if args.copy_calibration:
+        copy_calibration(device)
 
     secondary = {}
     for name in [s for s in args.secondary.split(",") if s]:

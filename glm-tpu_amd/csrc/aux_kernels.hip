@@ -202,18 +202,16 @@ hipError_t launch_synth_fp8(uint64_t seed, int32_t experts, int64_t n, int64_t k
                             uint8_t* bits, float* scales, hipStream_t stream) {
   const int64_t blocks = (int64_t)experts * (n / 128) * (k / 128);
   if (blocks == 0) return hipSuccess;
-  hipLaunchKernelGGL(synth_fp8_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, seed, n, k, sigma,
+  return launch_kernel(synth_fp8_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, seed, n, k, sigma,
                      bits, scales);
-  return hipGetLastError();
 }
 
 hipError_t launch_decode_fp8_table(const uint8_t* bits, const float* scale, int64_t n, int64_t k,
                                    int32_t block_n, int32_t block_k, uint16_t* out,
                                    hipStream_t stream) {
   if (n * k == 0) return hipSuccess;
-  hipLaunchKernelGGL(decode_fp8_table_kernel, grid_for(n * k, 256), dim3(256), 0, stream, bits, scale,
+  return launch_kernel(decode_fp8_table_kernel, grid_for(n * k, 256), dim3(256), 0, stream, bits, scale,
                      n, k, block_n, block_k, out);
-  return hipGetLastError();
 }
 
 hipError_t launch_gather_rows(const void* src, int64_t src_rows, int64_t row_bytes,
@@ -221,10 +219,9 @@ hipError_t launch_gather_rows(const void* src, int64_t src_rows, int64_t row_byt
                               void* dst, hipStream_t stream) {
   const int64_t words = row_bytes / 4;
   if (n * words == 0) return hipSuccess;
-  hipLaunchKernelGGL(gather_rows_kernel, grid_for(n * words, 256), dim3(256), 0, stream,
+  return launch_kernel(gather_rows_kernel, grid_for(n * words, 256), dim3(256), 0, stream,
                      static_cast<const uint32_t*>(src), src_rows, words, index, div, mask, n,
                      static_cast<uint32_t*>(dst));
-  return hipGetLastError();
 }
 
 hipError_t launch_pack_panel_rows(const void* src, int64_t src_rows, int64_t row_bytes,
@@ -234,19 +231,17 @@ hipError_t launch_pack_panel_rows(const void* src, int64_t src_rows, int64_t row
   const int64_t words = row_bytes / 4;
   const int64_t total = (int64_t)capacity * panel_rows * words;
   if (total == 0) return hipSuccess;
-  hipLaunchKernelGGL(pack_panel_rows_kernel, grid_for(total, 256), dim3(256), 0, stream,
+  return launch_kernel(pack_panel_rows_kernel, grid_for(total, 256), dim3(256), 0, stream,
                      static_cast<const uint32_t*>(src), src_rows, words, row_starts, live_counts,
                      capacity, panel_rows, static_cast<uint32_t*>(dst));
-  return hipGetLastError();
 }
 
 hipError_t launch_zero_rows(void* out, int64_t rows, int64_t row_bytes, const uint8_t* keep,
                             const uint8_t* valid, hipStream_t stream) {
   const int64_t words = row_bytes / 4;
   if (rows * words == 0) return hipSuccess;
-  hipLaunchKernelGGL(zero_rows_kernel, grid_for(rows * words, 256), dim3(256), 0, stream,
+  return launch_kernel(zero_rows_kernel, grid_for(rows * words, 256), dim3(256), 0, stream,
                      static_cast<uint32_t*>(out), rows, words, keep, valid);
-  return hipGetLastError();
 }
 
 hipError_t launch_combine_routes(const uint16_t* y, int64_t tokens, int32_t top_k, int64_t h,
@@ -254,16 +249,14 @@ hipError_t launch_combine_routes(const uint16_t* y, int64_t tokens, int32_t top_
                                  uint16_t* out, hipStream_t stream) {
   const int64_t total = tokens * (h / 8);
   if (total == 0) return hipSuccess;
-  hipLaunchKernelGGL(combine_routes_kernel, grid_for(total, 256), dim3(256), 0, stream, y, tokens,
+  return launch_kernel(combine_routes_kernel, grid_for(total, 256), dim3(256), 0, stream, y, tokens,
                      top_k, h, ids, experts, bf16_sum, out);
-  return hipGetLastError();
 }
 
 hipError_t launch_fill_u32(void* dst, int64_t words, uint32_t value, hipStream_t stream) {
   if (words == 0) return hipSuccess;
-  hipLaunchKernelGGL(fill_u32_kernel, grid_for(words, 256), dim3(256), 0, stream,
+  return launch_kernel(fill_u32_kernel, grid_for(words, 256), dim3(256), 0, stream,
                      static_cast<uint32_t*>(dst), words, value);
-  return hipGetLastError();
 }
 
 }  // namespace glm_moe

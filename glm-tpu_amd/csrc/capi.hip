@@ -13,6 +13,15 @@
 
 using namespace glm_moe;
 
+namespace glm_moe {
+
+LaunchEvents& next_launch_events() {
+  thread_local LaunchEvents armed;
+  return armed;
+}
+
+}  // namespace glm_moe
+
 namespace {
 
 thread_local std::string g_last_error;
@@ -91,10 +100,38 @@ RoutedLayout routed_layout(int64_t tokens, int32_t top_k, int32_t experts, int64
 
 hipStream_t as_stream(void* s) { return static_cast<hipStream_t>(s); }
 
-int record(void* const* events, int i, hipStream_t stream) {
-  if (events == nullptr) return GLM_MOE_OK;
-  return check_hip(hipEventRecord(static_cast<hipEvent_t>(events[i]), stream), "hipEventRecord");
-}
+// Stage timing of glm_moe_routed_experts_timed: stage i's kernel records
+// events[2i] at its start and events[2i + 1] at its end.
+enum Stage { kStagePlan = 0, kStageGateUp = 1, kStageDown = 2, kStageCombine = 3, kStages = 4 };
+
+struct StageTimer {
+  void* const* events;  // null: untimed call
+  uint32_t* timed;      // bit i set when stage i ran a kernel
+
+  LaunchEvents at(int stage) const {
+    LaunchEvents e;
+    if (events != nullptr) {
+      e.start = static_cast<hipEvent_t>(events[2 * stage]);
+      e.stop = static_cast<hipEvent_t>(events[2 * stage + 1]);
+    }
+    return e;
+  }
+  // arm the next launch with stage i's events
+  void arm(int stage) const {
+    if (events == nullptr) return;
+    next_launch_events() = at(stage);
+    *timed |= 1u << stage;
+  }
+  // after stage i: if no kernel took its events (nothing to launch), disarm
+  void done(int stage) const {
+    if (events == nullptr) return;
+    LaunchEvents& armed = next_launch_events();
+    if (armed.start != nullptr || armed.stop != nullptr) {
+      armed = LaunchEvents{};
+      *timed &= ~(1u << stage);
+    }
+  }
+};
 
 int routed_experts_impl(const uint16_t* hidden, int64_t tokens, int64_t hidden_size,
                         const int32_t* route_indices, const float* route_weights, int32_t top_k,
@@ -102,7 +139,7 @@ int routed_experts_impl(const uint16_t* hidden, int64_t tokens, int64_t hidden_s
                         const float* gate_scale, const uint8_t* up_bits, const float* up_scale,
                         const uint8_t* down_bits, const float* down_scale, uint32_t flags,
                         uint16_t* out, uint8_t* valid, void* workspace, size_t workspace_bytes,
-                        void* const* events, void* stream_ptr) {
+                        const StageTimer& timer, void* stream_ptr) {
   GLM_REQUIRE(tokens > 0 && top_k > 0 && num_experts > 0, "routed experts need tokens, top_k, experts > 0");
   GLM_REQUIRE(top_k <= num_experts, "top_k exceeds expert count");
   GLM_REQUIRE(num_experts <= kMaxExperts, "at most %d experts", kMaxExperts);
@@ -135,9 +172,7 @@ int routed_experts_impl(const uint16_t* hidden, int64_t tokens, int64_t hidden_s
   uint16_t* act = reinterpret_cast<uint16_t*>(ws + L.act);
   uint16_t* y = reinterpret_cast<uint16_t*>(ws + L.y);
 
-  int st = record(events, 0, stream);
-  if (st) return st;
-
+  if (timer.events) *timer.timed = 0;
   if (n <= kMaxDecodeRoutes && decode_path_fits(hidden_size, intermediate)) {
     // decode: two kernels that find their routes themselves and fuse the combine
     DecodeArgs d{};
@@ -161,11 +196,10 @@ int routed_experts_impl(const uint16_t* hidden, int64_t tokens, int64_t hidden_s
     d.act = act;
     d.out = out;
     d.valid = valid;
-    d.between_event = events ? events[2] : nullptr;
-    if ((st = record(events, 1, stream))) return st;
-    GLM_HIP(launch_decode_routed(d, stream), "decode launch");
-    if ((st = record(events, 3, stream))) return st;
-    return record(events, 4, stream);
+    const LaunchEvents stage_events[2] = {timer.at(kStageGateUp), timer.at(kStageDown)};
+    if (timer.events) *timer.timed = (1u << kStageGateUp) | (1u << kStageDown);
+    GLM_HIP(launch_decode_routed(d, stream, timer.events ? stage_events : nullptr), "decode launch");
+    return GLM_MOE_OK;
   }
 
   RoutePlanArgs p{};
@@ -186,8 +220,9 @@ int routed_experts_impl(const uint16_t* hidden, int64_t tokens, int64_t hidden_s
   p.tile_row = tile_row;
   p.tile_live = tile_live;
   p.tile_count = tile_count;
+  timer.arm(kStagePlan);
   GLM_HIP(launch_route_plan(p, stream), "route plan launch");
-  if ((st = record(events, 1, stream))) return st;
+  timer.done(kStagePlan);
 
   // Every route (with its safe id) is covered by exactly one tile, so every
   // row of act and y is written before it is read.
@@ -216,8 +251,9 @@ int routed_experts_impl(const uint16_t* hidden, int64_t tokens, int64_t hidden_s
   g.table_stride = 0;
   g.out_row_ids = nullptr;
   g.route_w = nullptr;
+  timer.arm(kStageGateUp);
   GLM_HIP(launch_grouped_gemm(g, shape, 2, kEpiSwiglu, stream), "gate/up launch");
-  if ((st = record(events, 2, stream))) return st;
+  timer.done(kStageGateUp);
 
   GroupedGemmArgs d{};
   d.experts = num_experts;
@@ -242,14 +278,17 @@ int routed_experts_impl(const uint16_t* hidden, int64_t tokens, int64_t hidden_s
   d.table_stride = 0;
   d.out_row_ids = sorted;
   d.route_w = route_weights;
+  timer.arm(kStageDown);
   GLM_HIP(launch_grouped_gemm(d, shape, 1, kEpiWeighted, stream), "down launch");
-  if ((st = record(events, 3, stream))) return st;
+  timer.done(kStageDown);
 
+  timer.arm(kStageCombine);
   GLM_HIP(launch_combine_routes(y, tokens, top_k, hidden_size,
                                 (flags & GLM_MOE_DROP_UNOWNED) ? route_indices : nullptr, num_experts,
                                 (flags & GLM_MOE_ROUTE_SUM_BF16) ? 1 : 0, out, stream),
           "combine launch");
-  return record(events, 4, stream);
+  timer.done(kStageCombine);
+  return GLM_MOE_OK;
 }
 
 }  // namespace
@@ -469,7 +508,7 @@ int glm_moe_routed_experts(const uint16_t* hidden, int64_t tokens, int64_t hidde
   return routed_experts_impl(hidden, tokens, hidden_size, route_indices, route_weights, top_k,
                              num_experts, intermediate, gate_bits, gate_scale, up_bits, up_scale,
                              down_bits, down_scale, flags, out, valid, workspace, workspace_bytes,
-                             nullptr, stream);
+                             StageTimer{nullptr, nullptr}, stream);
 }
 
 int glm_moe_routed_experts_timed(const uint16_t* hidden, int64_t tokens, int64_t hidden_size,
@@ -479,13 +518,14 @@ int glm_moe_routed_experts_timed(const uint16_t* hidden, int64_t tokens, int64_t
                                  const uint8_t* up_bits, const float* up_scale,
                                  const uint8_t* down_bits, const float* down_scale,
                                  uint32_t flags, uint16_t* out, uint8_t* valid, void* workspace,
-                                 size_t workspace_bytes, void* const* events, void* stream) {
-  GLM_REQUIRE(events != nullptr, "five events required");
-  for (int i = 0; i < 5; ++i) GLM_REQUIRE(events[i] != nullptr, "five events required");
+                                 size_t workspace_bytes, void* const* events, uint32_t* timed_stages,
+                                 void* stream) {
+  GLM_REQUIRE(events != nullptr && timed_stages != nullptr, "eight events and a stage mask required");
+  for (int i = 0; i < 2 * kStages; ++i) GLM_REQUIRE(events[i] != nullptr, "eight events required");
   return routed_experts_impl(hidden, tokens, hidden_size, route_indices, route_weights, top_k,
                              num_experts, intermediate, gate_bits, gate_scale, up_bits, up_scale,
                              down_bits, down_scale, flags, out, valid, workspace, workspace_bytes,
-                             events, stream);
+                             StageTimer{events, timed_stages}, stream);
 }
 
 int glm_moe_event_create(void** event) {

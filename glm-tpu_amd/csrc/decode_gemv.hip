@@ -422,7 +422,7 @@ bool decode_path_fits(int64_t hidden, int64_t intermediate) {
          intermediate <= (int64_t)kMaxWaveSteps * kStepK;
 }
 
-hipError_t launch_decode_routed(const DecodeArgs& a, hipStream_t stream) {
+hipError_t launch_decode_routed(const DecodeArgs& a, hipStream_t stream, const LaunchEvents* stage_events) {
   if (a.routes <= 0 || a.routes > kMaxDecodeRoutes || a.top_k <= 0 || a.routes % a.top_k != 0 ||
       !decode_path_fits(a.hidden, a.intermediate) || a.hidden % kScaleBlock != 0 ||
       a.intermediate % kScaleBlock != 0)
@@ -431,20 +431,16 @@ hipError_t launch_decode_routed(const DecodeArgs& a, hipStream_t stream) {
   const size_t gu_lds = sizeof(float) * kGateUpWaves * 2 * kGemvRows +
                         sizeof(uint16_t) * kGateUpWaves * xs_elems(gu_steps);
   const dim3 g1(a.routes, a.intermediate / kGemvRows);
-  hipLaunchKernelGGL((decode_gate_up_kernel<kGateUpWaves>), g1, dim3(64 * kGateUpWaves), gu_lds, stream, a,
-                     gu_steps);
-  hipError_t err = hipGetLastError();
+  if (stage_events) next_launch_events() = stage_events[0];
+  hipError_t err = launch_kernel(decode_gate_up_kernel<kGateUpWaves>, g1, dim3(64 * kGateUpWaves), gu_lds, stream,
+                                 a, gu_steps);
   if (err != hipSuccess) return err;
-  if (a.between_event) {
-    err = hipEventRecord(static_cast<hipEvent_t>(a.between_event), stream);
-    if (err != hipSuccess) return err;
-  }
   const int d_steps = (a.intermediate + kStepK - 1) / kStepK;
   const size_t d_lds = sizeof(float) * kMaxDecodeRoutes * kGemvRows +
                        sizeof(uint16_t) * kDownWaves * xs_elems(d_steps);
-  hipLaunchKernelGGL((decode_down_kernel<kDownWaves>), dim3(a.hidden / kGemvRows), dim3(64 * kDownWaves), d_lds,
-                     stream, a);
-  return hipGetLastError();
+  if (stage_events) next_launch_events() = stage_events[1];
+  return launch_kernel(decode_down_kernel<kDownWaves>, dim3(a.hidden / kGemvRows), dim3(64 * kDownWaves), d_lds,
+                       stream, a);
 }
 
 }  // namespace glm_moe

@@ -232,21 +232,17 @@ hipError_t launch_shape(const GroupedGemmArgs& a, int epilogue, hipStream_t stre
   const dim3 block(64 * WN * WK);
   switch (epilogue) {
     case kEpiStoreF32:
-      hipLaunchKernelGGL((grouped_fp8_gemm_kernel<TABLES, RG, XROWS, WN, WK, DEPTH, kEpiStoreF32>), grid, block, 0, stream, a);
-      break;
+      return launch_kernel(grouped_fp8_gemm_kernel<TABLES, RG, XROWS, WN, WK, DEPTH, kEpiStoreF32>, grid, block, 0, stream, a);
     case kEpiStoreBf16:
-      hipLaunchKernelGGL((grouped_fp8_gemm_kernel<TABLES, RG, XROWS, WN, WK, DEPTH, kEpiStoreBf16>), grid, block, 0, stream, a);
-      break;
+      return launch_kernel(grouped_fp8_gemm_kernel<TABLES, RG, XROWS, WN, WK, DEPTH, kEpiStoreBf16>, grid, block, 0, stream, a);
     case kEpiSwiglu:
       if constexpr (TABLES == 2) {
-        hipLaunchKernelGGL((grouped_fp8_gemm_kernel<TABLES, RG, XROWS, WN, WK, DEPTH, kEpiSwiglu>), grid, block, 0, stream, a);
-        break;
+        return launch_kernel(grouped_fp8_gemm_kernel<TABLES, RG, XROWS, WN, WK, DEPTH, kEpiSwiglu>, grid, block, 0, stream, a);
       }
       return hipErrorInvalidValue;
     case kEpiWeighted:
       if constexpr (TABLES == 1) {
-        hipLaunchKernelGGL((grouped_fp8_gemm_kernel<TABLES, RG, XROWS, WN, WK, DEPTH, kEpiWeighted>), grid, block, 0, stream, a);
-        break;
+        return launch_kernel(grouped_fp8_gemm_kernel<TABLES, RG, XROWS, WN, WK, DEPTH, kEpiWeighted>, grid, block, 0, stream, a);
       }
       return hipErrorInvalidValue;
     default:

@@ -198,21 +198,17 @@ hipError_t launch_wide_shape(const GroupedGemmArgs& a, int epilogue, hipStream_t
   const dim3 block(64 * WAVES);
   switch (epilogue) {
     case kEpiStoreF32:
-      hipLaunchKernelGGL((grouped_fp8_gemm_wide_kernel<TABLES, RG, CGMAX, WAVES, kEpiStoreF32>), grid, block, 0, stream, a);
-      break;
+      return launch_kernel(grouped_fp8_gemm_wide_kernel<TABLES, RG, CGMAX, WAVES, kEpiStoreF32>, grid, block, 0, stream, a);
     case kEpiStoreBf16:
-      hipLaunchKernelGGL((grouped_fp8_gemm_wide_kernel<TABLES, RG, CGMAX, WAVES, kEpiStoreBf16>), grid, block, 0, stream, a);
-      break;
+      return launch_kernel(grouped_fp8_gemm_wide_kernel<TABLES, RG, CGMAX, WAVES, kEpiStoreBf16>, grid, block, 0, stream, a);
     case kEpiSwiglu:
       if constexpr (TABLES == 2) {
-        hipLaunchKernelGGL((grouped_fp8_gemm_wide_kernel<TABLES, RG, CGMAX, WAVES, kEpiSwiglu>), grid, block, 0, stream, a);
-        break;
+        return launch_kernel(grouped_fp8_gemm_wide_kernel<TABLES, RG, CGMAX, WAVES, kEpiSwiglu>, grid, block, 0, stream, a);
       }
       return hipErrorInvalidValue;
     case kEpiWeighted:
       if constexpr (TABLES == 1) {
-        hipLaunchKernelGGL((grouped_fp8_gemm_wide_kernel<TABLES, RG, CGMAX, WAVES, kEpiWeighted>), grid, block, 0, stream, a);
-        break;
+        return launch_kernel(grouped_fp8_gemm_wide_kernel<TABLES, RG, CGMAX, WAVES, kEpiWeighted>, grid, block, 0, stream, a);
       }
       return hipErrorInvalidValue;
     default:

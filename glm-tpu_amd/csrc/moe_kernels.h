@@ -1,10 +1,39 @@
 // Internal launch interface between the C-ABI layer (capi.hip) and the kernels.
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <utility>
+
 namespace glm_moe {
+
+// ------------------------------------------------------------------ launches
+// Stage timing: a caller may arm a (start, stop) pair of HIP events for the
+// next kernel launched on this thread; the launch then records them at the
+// kernel's own start and end (hipExtLaunchKernelGGL), so the elapsed time is
+// the kernel's duration without event packets between kernels.
+struct LaunchEvents {
+  hipEvent_t start = nullptr;
+  hipEvent_t stop = nullptr;
+};
+LaunchEvents& next_launch_events();  // thread-local; defined in capi.hip
+
+template <typename... KArgs, typename... Args>
+hipError_t launch_kernel(void (*kernel)(KArgs...), dim3 grid, dim3 block, size_t lds, hipStream_t stream,
+                         Args&&... args) {
+  LaunchEvents& ev = next_launch_events();
+  if (ev.start != nullptr || ev.stop != nullptr) {
+    const LaunchEvents armed = ev;
+    ev = LaunchEvents{};
+    hipExtLaunchKernelGGL(kernel, grid, block, (uint32_t)lds, stream, armed.start, armed.stop, 0u,
+                          std::forward<Args>(args)...);
+  } else {
+    hipLaunchKernelGGL(kernel, grid, block, lds, stream, std::forward<Args>(args)...);
+  }
+  return hipGetLastError();
+}
 
 // ------------------------------------------------------------------ route plan
 constexpr int kPlanThreads = 1024;
@@ -128,12 +157,12 @@ struct DecodeArgs {
   uint16_t* act;               // workspace [routes, intermediate] bf16, flat route order
   uint16_t* out;               // [tokens, hidden] bf16
   uint8_t* valid;
-  void* between_event;         // nullable hipEvent_t recorded between the two kernels
 };
 // The decode kernels stage one wave's K range (<= 2048) in LDS: hidden <= 8192
 // (four waves split it), intermediate <= 2048.
 bool decode_path_fits(int64_t hidden, int64_t intermediate);
-hipError_t launch_decode_routed(const DecodeArgs& a, hipStream_t stream);
+// stage_events: null, or the armed events of the gate/up [0] and down [1] kernels.
+hipError_t launch_decode_routed(const DecodeArgs& a, hipStream_t stream, const LaunchEvents* stage_events);
 
 // ------------------------------------------------------------------ auxiliary
 hipError_t launch_decode_fp8_table(const uint8_t* bits, const float* scale, int64_t n, int64_t k,

@@ -275,21 +275,18 @@ hipError_t launch_route_plan(const RoutePlanArgs& a, hipStream_t stream) {
   // 60 KB at 1024 experts, 15 KB at 256.
   const size_t lds = sizeof(int) * (size_t)(3 * ep + kPlanWaves + 2) +
                      sizeof(uint16_t) * (size_t)kPlanWaves * ep + (size_t)kPlanWaves * ep;
-  hipLaunchKernelGGL(route_plan_kernel, dim3(1), dim3(kPlanThreads), lds, stream, a);
-  return hipGetLastError();
+  return launch_kernel(route_plan_kernel, dim3(1), dim3(kPlanThreads), lds, stream, a);
 }
 
 hipError_t launch_panel_plan(const PanelPlanArgs& a, hipStream_t stream) {
-  hipLaunchKernelGGL(panel_plan_kernel, dim3(1), dim3(kPlanThreads), 0, stream, a);
-  return hipGetLastError();
+  return launch_kernel(panel_plan_kernel, dim3(1), dim3(kPlanThreads), 0, stream, a);
 }
 
 hipError_t launch_slot_tiles(const int32_t* local_ids, const uint8_t* owned, int32_t slots,
                              int32_t experts, int32_t* tile_expert, int32_t* tile_row,
                              int32_t* tile_live, int32_t* tile_count, hipStream_t stream) {
-  hipLaunchKernelGGL(slot_tiles_kernel, dim3(1), dim3(64), 0, stream, local_ids, owned, slots,
+  return launch_kernel(slot_tiles_kernel, dim3(1), dim3(64), 0, stream, local_ids, owned, slots,
                      experts, tile_expert, tile_row, tile_live, tile_count);
-  return hipGetLastError();
 }
 
 }  // namespace glm_moe

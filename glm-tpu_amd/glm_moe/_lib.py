@@ -64,7 +64,8 @@ SIGNATURES: dict[str, tuple] = {
     "glm_moe_event_elapsed_ms": (ctypes.c_int, [_vp, _vp, ctypes.POINTER(_f)]),
     "glm_moe_routed_experts_timed": (
         ctypes.c_int,
-        [_vp, _i64, _i64, _vp, _vp, _i32, _i32, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _u32, _vp, _vp, _vp, _sz, _vp, _vp],
+        [_vp, _i64, _i64, _vp, _vp, _i32, _i32, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _u32, _vp, _vp, _vp, _sz, _vp,
+         ctypes.POINTER(_u32), _vp],
     ),
     "glm_moe_synthesize_fp8_weights": (ctypes.c_int, [ctypes.c_uint64, _i32, _i64, _i64, _f, _vp, _vp, _vp]),
 }

@@ -21,6 +21,7 @@ same GPU (hipBLASLt), at the reference's rounding points.
 
 from __future__ import annotations
 
+import ctypes
 from typing import Any, NamedTuple
 
 import torch
@@ -102,7 +103,9 @@ def restore_prefill_route_rows(sorted_values: torch.Tensor, routes: PrefillRoute
 
 
 class RoutedTimings(NamedTuple):
-    """Stage times (ms) of one ``routed_experts`` call, measured with HIP events."""
+    """Kernel times (ms) of one ``routed_experts`` call per stage, from HIP events
+    the kernels record at their own start and end; a stage that ran no kernel
+    (the decode path has no separate plan or combine) is 0."""
 
     plan: float
     gate_up: float
@@ -115,26 +118,32 @@ class RoutedTimings(NamedTuple):
 
 
 class StageEvents:
-    """Five HIP events recorded around the stages of ``routed_experts``."""
+    """A start and a stop HIP event for each of the four stages of ``routed_experts``."""
+
+    STAGES = 4
 
     def __init__(self) -> None:
         import ctypes
 
         self._handles = []
-        for _ in range(5):
+        for _ in range(2 * self.STAGES):
             slot = ctypes.c_void_p()
             _lib.call("glm_moe_event_create", ctypes.byref(slot))
             self._handles.append(slot.value)
-        self.array = (ctypes.c_void_p * 5)(*self._handles)
+        self.array = (ctypes.c_void_p * (2 * self.STAGES))(*self._handles)
+        self.timed = ctypes.c_uint32(0)
 
     def elapsed(self) -> RoutedTimings:
         import ctypes
 
         ms = []
-        for i in range(4):
+        for i in range(self.STAGES):
+            if not (self.timed.value >> i) & 1:
+                ms.append(0.0)
+                continue
             value = ctypes.c_float()
-            _lib.call("glm_moe_event_elapsed_ms", ctypes.c_void_p(self._handles[i]),
-                      ctypes.c_void_p(self._handles[i + 1]), ctypes.byref(value))
+            _lib.call("glm_moe_event_elapsed_ms", ctypes.c_void_p(self._handles[2 * i]),
+                      ctypes.c_void_p(self._handles[2 * i + 1]), ctypes.byref(value))
             ms.append(value.value)
         return RoutedTimings(*ms)
 
@@ -229,7 +238,8 @@ def routed_experts(
     if events is None:
         _lib.call("glm_moe_routed_experts", *args, _lib.stream_of(hidden))
     else:
-        _lib.call("glm_moe_routed_experts_timed", *args, events.array, _lib.stream_of(hidden))
+        _lib.call("glm_moe_routed_experts_timed", *args, events.array, ctypes.byref(events.timed),
+                  _lib.stream_of(hidden))
     return out, valid
 
 

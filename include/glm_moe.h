@@ -137,10 +137,13 @@ int glm_moe_routed_experts(const uint16_t* hidden, int64_t tokens, int64_t hidde
                            void* stream);
 
 /* Stage timing for benchmarks: glm_moe_routed_experts_timed is
- * glm_moe_routed_experts with a HIP event recorded on `stream` before the
- * route plan and after each of its four stages (plan, gate/up, down, combine):
- * events[0..4], created with glm_moe_event_create.  No reference counterpart
- * (the reference labels its kernels for the TPU profiler, kernels/names.py). */
+ * glm_moe_routed_experts whose kernels record HIP events at their own start
+ * and end (hipExtLaunchKernelGGL): the kernel of stage i (0 route plan,
+ * 1 gate/up, 2 down, 3 combine) records events[2i] and events[2i + 1], and
+ * bit i of *timed_stages is set when stage i ran a kernel (the decode path
+ * has no separate plan or combine kernel).  Events come from
+ * glm_moe_event_create.  No reference counterpart (the reference labels its
+ * kernels for the TPU profiler, glm_tpu/kernels/names.py:1-31). */
 int glm_moe_event_create(void** event);
 int glm_moe_event_destroy(void* event);
 int glm_moe_event_elapsed_ms(void* start, void* stop, float* ms);
@@ -151,7 +154,8 @@ int glm_moe_routed_experts_timed(const uint16_t* hidden, int64_t tokens, int64_t
                                  const uint8_t* up_bits, const float* up_scale,
                                  const uint8_t* down_bits, const float* down_scale,
                                  uint32_t flags, uint16_t* out, uint8_t* valid, void* workspace,
-                                 size_t workspace_bytes, void* const* events, void* stream);
+                                 size_t workspace_bytes, void* const* events, uint32_t* timed_stages,
+                                 void* stream);
 
 /* Synthetic FP8 expert tables for tests and benchmarks, the reference's fixture
  * recipe (tools/equivalence/fixture.py:158-172) with 128x128 block scales:
