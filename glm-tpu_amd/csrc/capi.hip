@@ -76,7 +76,7 @@ int64_t max_tiles_for(int64_t routes, int32_t experts, int rows) {
 
 // Byte layout of the glm_moe_routed_experts workspace.
 struct RoutedLayout {
-  size_t sorted, inverse, counts, offsets, tiles, act, y, total;
+  size_t sorted, inverse, counts, offsets, tiles, expert_tiles, act, y, total;
   int64_t max_tiles;
 };
 
@@ -92,6 +92,7 @@ RoutedLayout routed_layout(int64_t tokens, int32_t top_k, int32_t experts, int64
   L.counts = off;  off = align_up(off + sizeof(int32_t) * experts);
   L.offsets = off; off = align_up(off + sizeof(int32_t) * (experts + 1));
   L.tiles = off;   off = align_up(off + sizeof(int32_t) * (3 * L.max_tiles + 1));
+  L.expert_tiles = off; off = align_up(off + sizeof(int32_t) * 2 * experts);
   L.act = off;     off = align_up(off + sizeof(uint16_t) * n * intermediate);
   L.y = off;       off = align_up(off + sizeof(uint16_t) * n * hidden);
   L.total = off;
@@ -169,6 +170,8 @@ int routed_experts_impl(const uint16_t* hidden, int64_t tokens, int64_t hidden_s
   int32_t* tile_row = tile_expert + L.max_tiles;
   int32_t* tile_live = tile_row + L.max_tiles;
   int32_t* tile_count = tile_live + L.max_tiles;
+  int32_t* expert_first_tile = reinterpret_cast<int32_t*>(ws + L.expert_tiles);
+  int32_t* expert_tiles = expert_first_tile + num_experts;
   uint16_t* act = reinterpret_cast<uint16_t*>(ws + L.act);
   uint16_t* y = reinterpret_cast<uint16_t*>(ws + L.y);
 
@@ -220,6 +223,8 @@ int routed_experts_impl(const uint16_t* hidden, int64_t tokens, int64_t hidden_s
   p.tile_row = tile_row;
   p.tile_live = tile_live;
   p.tile_count = tile_count;
+  p.expert_first_tile = expert_first_tile;
+  p.expert_tiles = expert_tiles;
   timer.arm(kStagePlan);
   GLM_HIP(launch_route_plan(p, stream), "route plan launch");
   timer.done(kStagePlan);
@@ -245,6 +250,8 @@ int routed_experts_impl(const uint16_t* hidden, int64_t tokens, int64_t hidden_s
   g.tile_live = tile_live;
   g.tile_count = tile_count;
   g.max_tiles = (int32_t)L.max_tiles;
+  g.expert_first_tile = expert_first_tile;
+  g.expert_tiles = expert_tiles;
   g.valid = nullptr;
   g.out = act;
   g.ldo = intermediate;
@@ -272,6 +279,8 @@ int routed_experts_impl(const uint16_t* hidden, int64_t tokens, int64_t hidden_s
   d.tile_live = tile_live;
   d.tile_count = tile_count;
   d.max_tiles = (int32_t)L.max_tiles;
+  d.expert_first_tile = expert_first_tile;
+  d.expert_tiles = expert_tiles;
   d.valid = nullptr;
   d.out = y;
   d.ldo = hidden_size;

@@ -1,0 +1,365 @@
+// Prefill route-grouped FP8 projection: tiles of up to 128 sorted routes.
+//
+// Same arithmetic as every projection of this library (weights decoded as
+// bf16(f32(e4m3) * block scale), bf16 activations, FP32 accumulation over
+// ascending 128-wide K blocks on v_mfma_f32_16x16x32_bf16) -- the projection
+// of glm-tpu's prefill_panel_fp8_matmul (reference
+// glm_tpu/kernels/fp8_grouped_matmul/panel_kernel.py:83-101).
+//
+// Work item = (expert, tile of <= 128 sorted routes, stripe of BN weight rows).
+//   * Each of the WAVES waves owns RG x 16 rows of every table of the stripe.
+//     It loads them straight into registers in MFMA A layout (lane l: row l%16,
+//     16 bytes at K offset (l/16)*16 and 64 + (l/16)*16 of the block), STAGES
+//     K blocks ahead, and decodes each byte once.  A weight byte is therefore
+//     read from HBM and decoded exactly once per work item.
+//   * The tile's activation rows (gathered token rows for gate/up, sorted
+//     activation rows for down) go HBM/L2 -> LDS with direct-to-LDS loads
+//     (global_load_lds_dwordx4, no registers) into a ring of STAGES K blocks.
+//     Each 1 KB load covers 4 rows x 256 bytes; chunk c of row r is stored in
+//     slot c ^ (r % 16), so that the 16 lanes reading one MFMA B fragment hit
+//     distinct banks.  All waves share the staged rows as the B operand.
+//   * One workgroup barrier per K block; when it is passed, the block's rows
+//     are in LDS and every wave has finished with the block STAGES - 1 back,
+//     whose slot is refilled next.
+// Work items are ordered expert-major, then stripe, then route tile, and
+// laid out XCD-aware: workgroup b runs on XCD b % 8, and XCD x walks the
+// contiguous range [x * per, (x + 1) * per) of work items, so the tiles that
+// share an expert's weight stripe (hot experts) or the stripes that share a
+// tile's activation rows run together on one XCD and meet in its L2.
+#include <type_traits>
+
+#include "gemm_epilogue.h"
+#include "moe_common.h"
+#include "moe_kernels.h"
+
+namespace glm_moe {
+
+namespace {
+
+__device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
+
+constexpr int kNonTemporal = 2;             // buffer load cache policy: streamed once (nt)
+constexpr int kBufferFormat = 0x00020000;   // raw buffer descriptor word 3: 32-bit data format
+
+constexpr int kBM = 128;           // routes per tile
+constexpr int kCG = kBM / 16;      // 16-route column groups
+constexpr int kXcds = 8;           // MI355X: 8 XCDs, workgroups dealt round-robin
+constexpr int kRowBytes = kScaleBlock * 2;   // one staged activation row of a K block (bf16)
+constexpr int kStageBytes = kBM * kRowBytes; // 32 KB
+
+// This wave's loads but the newest N have completed (direct-to-LDS loads
+// included: their data is in LDS); its LDS reads have completed; then the
+// workgroup barrier.  Unlike __syncthreads() this does not wait for every
+// outstanding load, so the weight and activation prefetches of later K blocks
+// stay in flight across the barrier.  Inline asm with a memory clobber: the
+// compiler moves no memory access across it.
+template <int N>
+__device__ __forceinline__ void wait_loads_then_barrier() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(N) : "memory");
+}
+
+__device__ __forceinline__ void wait_all_loads() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+// 16 bytes a lane from rsrc + voffset + soffset straight into LDS at
+// lds + 16 * lane (buffer_load_dwordx4 ... lds).  The builtin only exists for
+// the device target; the host pass of the kernel template must not see it.
+__device__ __forceinline__ void load_lds_16(__amdgpu_buffer_rsrc_t rsrc, uint8_t* lds, int voffset, int soffset) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (__attribute__((address_space(3))) void*)lds, 16, voffset, soffset,
+                                           0, 0);
+#endif
+}
+
+template <int TABLES, int RG, int WAVES, int STAGES, int EPI>
+__global__ __launch_bounds__(64 * WAVES, 1) void prefill_gemm_kernel(const GroupedGemmArgs a) {
+  constexpr int BN = WAVES * RG * 16;                      // weight rows per table per work item
+  constexpr int XLOADS = kStageBytes / (WAVES * 1024);     // 1 KB activation loads per wave per K block
+  constexpr int WLOADS = TABLES * RG * 2;                  // 16-byte weight loads per lane per K block
+  // vector-memory loads a wave issues per K block (activations and weights, in any order)
+  constexpr int PER_BLOCK = XLOADS + WLOADS;
+  static_assert(XLOADS * WAVES * 1024 == kStageBytes, "activation stage split");
+  static_assert(STAGES % 2 == 0, "A operands alternate between two buffers");
+  // block kb is complete once at most the STAGES - 2 blocks issued after it are in flight
+  constexpr int X_PENDING = (STAGES - 2) * PER_BLOCK;
+  // [STAGES][kBM][256 B] activation ring, then per wave [TABLES * RG][16 rows][128 B] weight transposes
+  extern __shared__ __attribute__((aligned(16))) uint8_t xs[];
+
+  if (a.valid != nullptr && a.valid[0] == 0) return;
+  const int stripes = a.n / BN;
+  const int total = stripes * a.tile_count[0];
+  const int per = (total + kXcds - 1) / kXcds;
+  const int b = blockIdx.x;
+  if (b / kXcds >= per) return;
+  const int item = (b % kXcds) * per + b / kXcds;
+  if (item >= total) return;
+  // work-item scalars are workgroup-uniform: readfirstlane keeps them (and the
+  // addresses derived from them) in scalar registers
+  const int e = uniform(a.tile_expert[item / stripes]);
+  if (e < 0 || e >= a.experts) return;
+  const int t0 = uniform(a.expert_first_tile[e]);
+  const int nt = uniform(a.expert_tiles[e]);
+  if (nt <= 0) return;
+  const int rel = item - stripes * t0;
+  const int stripe = rel / nt;
+  const int tile = t0 + rel % nt;
+  if (stripe < 0 || stripe >= stripes || tile >= a.max_tiles) return;
+  const int r0 = uniform(a.tile_row[tile]);
+  const int live = uniform(a.tile_live[tile]);
+  // A consistent plan always passes; a corrupt one computes nothing instead of
+  // reading out of bounds.
+  if (uniform(a.tile_expert[tile]) != e || r0 < 0 || live <= 0 || live > kBM || r0 + live > a.rows) return;
+  const int ncg = (live + 15) >> 4;
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lrow = lane & 15;
+  const int lgrp = lane >> 4;
+  const int N = a.n;
+  const int K = a.k;
+  const int KB = K / kScaleBlock;
+  const int n0 = stripe * BN + wave * RG * 16;
+
+  // Loads are raw buffer loads: a loop-invariant per-lane VGPR offset, the K
+  // block as a scalar offset, the base and bounds in a scalar descriptor.
+  // ---- activation rows this lane loads: instruction i of a stage covers rows
+  // 4 * (wave * XLOADS + i) + lane / 16; the lane fetches the chunk whose slot is lane % 16
+  const __amdgpu_buffer_rsrc_t xrsrc = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t*>(a.x), (short)0, (int)(a.x_rows * K * 2), kBufferFormat);
+  int xoff[XLOADS];
+#pragma unroll
+  for (int i = 0; i < XLOADS; ++i) {
+    const int row = 4 * (wave * XLOADS + i) + lgrp;
+    const int r = r0 + (row < live ? row : 0);  // padding rows repeat a live row; their columns are dropped
+    int64_t phys = a.x_row_ids ? a.x_row_ids[r] / a.x_row_div : r;
+    phys = phys < 0 ? 0 : (phys >= a.x_rows ? a.x_rows - 1 : phys);
+    xoff[i] = (int)(phys * K * 2) + ((lrow ^ (row & 15)) << 4);
+  }
+
+  // ---- weight rows of this wave: row n0 + rg * 16 + lane % 16, bytes (lane / 16) * 16 (+ 64);
+  // block scales of the rows' K blocks one per lane (lane kb holds block kb;
+  // K <= 64 blocks), picked per block with v_readlane
+  __amdgpu_buffer_rsrc_t wrsrc[TABLES][RG];
+  float sreg[TABLES][RG];
+  // 8 rows x 128 bytes per load (lane l: row 8h + l/8 of the 16, chunk l%8):
+  // every 128-byte line is fetched whole by one instruction, the pattern that
+  // streams HBM at full rate (half lines per instruction cap near 5.4 TB/s)
+  int woff[2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) woff[h] = (8 * h + (lane >> 3)) * K + (lane & 7) * 16;
+#pragma unroll
+  for (int t = 0; t < TABLES; ++t) {
+    const uint8_t* wb = t == 0 ? a.w0 : a.w1;
+    const float* sb = t == 0 ? a.s0 : a.s1;
+#pragma unroll
+    for (int rg = 0; rg < RG; ++rg) {
+      wrsrc[t][rg] = __builtin_amdgcn_make_buffer_rsrc(
+          const_cast<uint8_t*>(wb + ((size_t)e * N + n0 + rg * 16) * (size_t)K), (short)0, 16 * K, kBufferFormat);
+      const float* srow = sb + ((size_t)e * (N / kScaleBlock) + (n0 + rg * 16) / kScaleBlock) * KB;
+      sreg[t][rg] = lane < KB ? srow[lane] : 0.0f;
+    }
+  }
+
+  f32x4 acc[TABLES][RG][kCG];
+#pragma unroll
+  for (int t = 0; t < TABLES; ++t)
+#pragma unroll
+    for (int rg = 0; rg < RG; ++rg)
+#pragma unroll
+      for (int cg = 0; cg < kCG; ++cg) acc[t][rg][cg] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  // weights: two ring slots; block kb + 2 is issued while block kb + 1 is decoded
+  u32x4 wring[2][TABLES][RG][2];
+
+  // Issue block kb's activations into stage st, and block kw's weights into
+  // ring slot kw % 2 (both clamped to the last block: the pipeline always
+  // issues the same number of loads, so the wait counts stay exact).
+  auto issue = [&](int st, int kb, int kw) {
+    kb = kb < KB ? kb : KB - 1;
+    const int ws = kw & 1;
+    kw = kw < KB ? kw : KB - 1;
+    uint8_t* stage = xs + st * kStageBytes;
+#pragma unroll
+    for (int i = 0; i < XLOADS; ++i)
+      load_lds_16(xrsrc, stage + (wave * XLOADS + i) * 1024, xoff[i], kb * kRowBytes);
+#pragma unroll
+    for (int t = 0; t < TABLES; ++t)
+#pragma unroll
+      for (int rg = 0; rg < RG; ++rg) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+          wring[ws][t][rg][h] = __builtin_bit_cast(
+              u32x4, __builtin_amdgcn_raw_buffer_load_b128(wrsrc[t][rg], woff[h], kw * kScaleBlock, kNonTemporal));
+      }
+  };
+
+  // Software pipeline inside each wave: while the MFMAs of block kb run (A
+  // operands decoded one block earlier), the VALU decodes block kb + 1 into the
+  // other A buffer, so the matrix cores and the vector ALU work at the same
+  // time.  The column-group count is a compile-time constant of each variant
+  // (2, 4, 6 or 8 groups of 16 routes), so the body has no branches and the
+  // scheduler may interleave ds_read, MFMA and decode instructions freely.
+  auto run = [&](auto ncg_tag) {
+    constexpr int NCG = decltype(ncg_tag)::value;
+    constexpr int NOPS = TABLES * RG * 4;  // bf16x8 A operands per block
+    bf16x8 A[2][TABLES][RG][4];
+    // Ring slot -> the wave's own LDS region (chunk c of row r in slot c ^ (r % 8))
+    // -> registers in MFMA A layout: lane l gets row l % 16, chunks l/16 and
+    // 4 + l/16 (K = g*16 .. +15 and 64 + g*16 .. +15 of the block).  Only this
+    // wave touches the region, and its LDS accesses run in order: no barrier.
+    uint8_t* wl = xs + STAGES * kStageBytes + wave * (TABLES * RG * 2048);
+    auto transpose = [&](int slot, u32x4 (&wt)[TABLES][RG][2]) {
+#pragma unroll
+      for (int t = 0; t < TABLES; ++t)
+#pragma unroll
+        for (int rg = 0; rg < RG; ++rg)
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            const int row = 8 * h + (lane >> 3);
+            *reinterpret_cast<u32x4*>(wl + (t * RG + rg) * 2048 + row * 128 + (((lane & 7) ^ (row & 7)) << 4)) =
+                wring[slot][t][rg][h];
+          }
+#pragma unroll
+      for (int t = 0; t < TABLES; ++t)
+#pragma unroll
+        for (int rg = 0; rg < RG; ++rg)
+#pragma unroll
+          for (int h = 0; h < 2; ++h)
+            wt[t][rg][h] = *reinterpret_cast<const u32x4*>(wl + (t * RG + rg) * 2048 + lrow * 128 +
+                                                            (((lgrp + 4 * h) ^ (lrow & 7)) << 4));
+    };
+    auto decode_op = [&](int o, const u32x4 (&wt)[TABLES][RG][2], float (&sc)[TABLES][RG],
+                         bf16x8 (&dst)[TABLES][RG][4]) {
+      const int t = o / (RG * 4), rg = (o / 4) % RG, q = o % 4;
+      const u32x4 w = wt[t][rg][q >> 1];
+      dst[t][rg][q] = (q & 1) ? decode_fp8x8(w.z, w.w, sc[t][rg]) : decode_fp8x8(w.x, w.y, sc[t][rg]);
+    };
+    auto scales_of = [&](int kb, float (&sc)[TABLES][RG]) {
+      kb = kb < KB ? kb : KB - 1;
+#pragma unroll
+      for (int t = 0; t < TABLES; ++t)
+#pragma unroll
+        for (int rg = 0; rg < RG; ++rg)
+          sc[t][rg] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, sreg[t][rg]), kb));
+    };
+    // MFMAs of the block staged in `st` with operands A[cur]; decode of ring
+    // slot `next_slot` (block kb_next) into A[cur ^ 1], spread over the column groups
+    auto step = [&](int st, int cur, int next_slot, int kb_next) {
+      const uint8_t* stage = xs + st * kStageBytes;
+      float sc[TABLES][RG];
+      scales_of(kb_next, sc);
+      u32x4 wt[TABLES][RG][2];
+      transpose(next_slot, wt);
+#pragma unroll
+      for (int cg = 0; cg < NCG; ++cg) {
+        // B fragment j of route row i: logical chunks 2g, 2g+1, 8+2g, 8+2g+1 (the A K order)
+        const int i = cg * 16 + lrow;
+        const uint8_t* rowp = stage + i * kRowBytes;
+        const int sw = i & 15;
+        const bf16x8 b0 = as_bf16x8(*reinterpret_cast<const u32x4*>(rowp + (((2 * lgrp) ^ sw) << 4)));
+        const bf16x8 b1 = as_bf16x8(*reinterpret_cast<const u32x4*>(rowp + (((2 * lgrp + 1) ^ sw) << 4)));
+        const bf16x8 b2 = as_bf16x8(*reinterpret_cast<const u32x4*>(rowp + (((8 + 2 * lgrp) ^ sw) << 4)));
+        const bf16x8 b3 = as_bf16x8(*reinterpret_cast<const u32x4*>(rowp + (((9 + 2 * lgrp) ^ sw) << 4)));
+#pragma unroll
+        for (int t = 0; t < TABLES; ++t)
+#pragma unroll
+          for (int rg = 0; rg < RG; ++rg) {
+            f32x4 c = acc[t][rg][cg];
+            c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[cur][t][rg][0], b0, c, 0, 0, 0);
+            c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[cur][t][rg][1], b1, c, 0, 0, 0);
+            c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[cur][t][rg][2], b2, c, 0, 0, 0);
+            c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[cur][t][rg][3], b3, c, 0, 0, 0);
+            acc[t][rg][cg] = c;
+          }
+#pragma unroll
+        for (int o = cg * NOPS / NCG; o < (cg + 1) * NOPS / NCG; ++o) decode_op(o, wt, sc, A[cur ^ 1]);
+        // one column group at a time: the next group's B reads are not hoisted
+        // above this one (bounds the registers they hold)
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    };
+
+    // prologue: activations of blocks 0 .. STAGES-2 and weights of blocks 0
+    // and 1 in flight (STAGES - 1 >= 2 issues), block 0 decoded
+#pragma unroll
+    for (int st = 0; st < STAGES - 1; ++st) issue(st, st, st < 2 ? st : 1);
+    {
+      float sc[TABLES][RG];
+      scales_of(0, sc);
+      u32x4 wt[TABLES][RG][2];
+      transpose(0, wt);
+#pragma unroll
+      for (int o = 0; o < NOPS; ++o) decode_op(o, wt, sc, A[0]);
+    }
+    // K loop unrolled by STAGES (KB % STAGES == 0) so that ring slots and A buffers are static
+    for (int kb0 = 0; kb0 < KB; kb0 += STAGES) {
+#pragma unroll
+      for (int j = 0; j < STAGES; ++j) {
+        const int kb = kb0 + j;
+        // this wave's share of block kb has landed; after the barrier everyone's
+        // has, and everyone is done with block kb - 1, whose slot is refilled now
+        wait_loads_then_barrier<X_PENDING>();
+        issue((j + STAGES - 1) % STAGES, kb + STAGES - 1, kb + 2);
+        step(j, j & 1, (j + 1) & 1, kb + 1);
+      }
+    }
+  };
+  if (ncg <= 2) run(std::integral_constant<int, 2>{});
+  else if (ncg <= 4) run(std::integral_constant<int, 4>{});
+  else if (ncg <= 6) run(std::integral_constant<int, 6>{});
+  else run(std::integral_constant<int, 8>{});
+  wait_all_loads();  // no load may still target LDS when the workgroup ends
+
+  // Epilogue: lane holds rows n .. n+3 of route column cg*16 + lrow.
+#pragma unroll
+  for (int cg = 0; cg < kCG; ++cg) {
+    const int col = cg * 16 + lrow;
+    if (cg >= ncg || col >= live) continue;
+#pragma unroll
+    for (int rg = 0; rg < RG; ++rg)
+      store_fragment<TABLES, EPI>(a, r0 + col, n0 + rg * 16 + lgrp * 4, acc[0][rg][cg], acc[TABLES - 1][rg][cg]);
+  }
+}
+
+template <int TABLES, int RG, int WAVES, int STAGES, int EPI>
+hipError_t launch_prefill(const GroupedGemmArgs& a, hipStream_t stream) {
+  constexpr int BN = WAVES * RG * 16;
+  const size_t lds = (size_t)STAGES * kStageBytes + (size_t)WAVES * TABLES * RG * 2048;
+  static bool attr_set = false;  // one attribute call per instantiation (idempotent)
+  if (!attr_set) {
+    const hipError_t err = hipFuncSetAttribute(
+        reinterpret_cast<const void*>(prefill_gemm_kernel<TABLES, RG, WAVES, STAGES, EPI>),
+        hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (err != hipSuccess) return err;
+    attr_set = true;
+  }
+  const int64_t items = (int64_t)(a.n / BN) * a.max_tiles;
+  const int64_t grid = (items + kXcds - 1) / kXcds * kXcds;
+  return launch_kernel(prefill_gemm_kernel<TABLES, RG, WAVES, STAGES, EPI>, dim3((unsigned)grid), dim3(64 * WAVES),
+                       lds, stream, a);
+}
+
+}  // namespace
+
+// Weight rows per table per work item of the prefill kernel.
+int prefill_bn(int tables) { return tables == 2 ? 8 * 16 : 8 * 32; }
+
+constexpr int kPrefillStages = 4;
+
+// The prefill kernel holds one block scale per lane (K <= 64 blocks of 128)
+// and unrolls its K loop by its stage count (K blocks a multiple of it).
+bool prefill_fits(int64_t n, int64_t k, int tables) {
+  return n % prefill_bn(tables) == 0 && k % kScaleBlock == 0 && k / kScaleBlock <= 64 &&
+         (k / kScaleBlock) % kPrefillStages == 0;
+}
+
+hipError_t launch_grouped_gemm_prefill(const GroupedGemmArgs& a, int tables, int epilogue, hipStream_t stream) {
+  if (a.max_tiles <= 0) return hipSuccess;
+  if (a.expert_first_tile == nullptr || a.expert_tiles == nullptr) return hipErrorInvalidValue;
+  if (!prefill_fits(a.n, a.k, tables)) return hipErrorInvalidValue;
+  if (tables == 2 && epilogue == kEpiSwiglu) return launch_prefill<2, 1, 8, kPrefillStages, kEpiSwiglu>(a, stream);
+  if (tables == 1 && epilogue == kEpiWeighted) return launch_prefill<1, 2, 8, kPrefillStages, kEpiWeighted>(a, stream);
+  return hipErrorInvalidValue;
+}
+
+}  // namespace glm_moe

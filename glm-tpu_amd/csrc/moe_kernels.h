@@ -59,6 +59,8 @@ struct RoutePlanArgs {
   int32_t* tile_row;
   int32_t* tile_live;
   int32_t* tile_count;       // [1]
+  int32_t* expert_first_tile;  // nullable [experts]: first tile of each expert
+  int32_t* expert_tiles;       // nullable [experts]: tiles of each expert
 };
 hipError_t launch_route_plan(const RoutePlanArgs& a, hipStream_t stream);
 
@@ -112,6 +114,8 @@ struct GroupedGemmArgs {
   const int32_t* tile_live;
   const int32_t* tile_count;
   int32_t max_tiles;
+  const int32_t* expert_first_tile;  // prefill kernel: first work-list tile of each expert
+  const int32_t* expert_tiles;       // prefill kernel: work-list tiles of each expert
   const uint8_t* valid;        // nullable: no work at all when *valid == 0
   void* out;
   int64_t ldo;                 // elements between output rows
@@ -130,6 +134,11 @@ enum GemmShape : int {
 int gemm_shape_rows(int shape);
 int gemm_shape_bn(int shape, int tables);
 hipError_t launch_grouped_gemm_wide(const GroupedGemmArgs& a, int tables, int epilogue, hipStream_t stream);
+// The pipelined prefill kernel (<= 128 routes per tile, expert-major XCD-aware
+// work order); needs the plan's expert_first_tile / expert_tiles.
+int prefill_bn(int tables);
+bool prefill_fits(int64_t n, int64_t k, int tables);
+hipError_t launch_grouped_gemm_prefill(const GroupedGemmArgs& a, int tables, int epilogue, hipStream_t stream);
 hipError_t launch_grouped_gemm(const GroupedGemmArgs& a, int shape, int tables, int epilogue,
                                hipStream_t stream);
 

@@ -163,6 +163,8 @@ __global__ __launch_bounds__(kPlanThreads) void route_plan_kernel(const RoutePla
     const int t0 = block_exclusive_scan(nt, s_scan, &total);
     if (tid < E) {
       const int start = s_off[tid];
+      if (a.expert_first_tile) a.expert_first_tile[tid] = t0;
+      if (a.expert_tiles) a.expert_tiles[tid] = nt;
       for (int j = 0; j < nt; ++j) {
         const int idx = t0 + j;
         if (idx < a.max_tiles) {
