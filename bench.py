@@ -35,6 +35,7 @@ sys.path.insert(0, str(ROOT))
 
 HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0
+FP8_PEAK_TFLOPS = 5000.0
 ROTATIONS = 64
 TABLE_KEYS = ("gate_bits", "gate_scale", "up_bits", "up_scale", "down_bits", "down_scale")
 
@@ -45,8 +46,11 @@ def parse_args():
     p.add_argument("--steps", type=int, default=100)
     p.add_argument("--warmup", type=int, default=10)
     p.add_argument("--config", default="decode_t1")
-    p.add_argument("--secondary", default="decode_t4,prefill_t2048,prefill_t8192_zipf",
-                   help="comma-separated extra configs measured after the headline ('' for none)")
+    p.add_argument("--secondary",
+                   default="decode_t4,prefill_t2048,prefill_t8192_zipf,prefill_t2048:fp8,prefill_t8192_zipf:fp8",
+                   help="comma-separated extra configs measured after the headline ('' for none); a ':fp8' "
+                        "suffix runs the native FP8 MFMA mode and reports its error against the reference "
+                        "numerics on sampled tokens")
     p.add_argument("--secondary-steps", type=int, default=20)
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--copy-calibration", action="store_true",
@@ -70,12 +74,13 @@ def copy_calibration(device, nbytes=1 << 30, times=3):
 class Workload:
     """Rotated synthetic routings of one config on the device, plus their costs."""
 
-    def __init__(self, cfg, tables, device, rotations=ROTATIONS, seed0=1000):
+    def __init__(self, cfg, tables, device, rotations=ROTATIONS, seed0=1000, activations="bfloat16"):
         import torch
 
         from glm_moe import synthetic as S
 
         self.cfg = cfg
+        self.activations = activations
         self.tables = tables
         self.inputs = []
         self.host = []
@@ -105,7 +110,7 @@ def run_steps(work, steps, warmup, with_stage_events=True):
     n_rot = len(work.inputs)
     for i in range(warmup):
         x, ids, w = work.inputs[i % n_rot]
-        routed_experts(x, ids, w, *tables, out=out)
+        routed_experts(x, ids, w, *tables, out=out, activations=work.activations)
     events = [StageEvents() for _ in range(steps)] if with_stage_events else [None] * steps
     start = torch.cuda.Event(enable_timing=True)
     stop = torch.cuda.Event(enable_timing=True)
@@ -113,7 +118,7 @@ def run_steps(work, steps, warmup, with_stage_events=True):
     start.record()
     for i in range(steps):
         x, ids, w = work.inputs[(warmup + i) % n_rot]
-        routed_experts(x, ids, w, *tables, out=out, events=events[i])
+        routed_experts(x, ids, w, *tables, out=out, events=events[i], activations=work.activations)
     stop.record()
     torch.cuda.synchronize()
     ms = start.elapsed_time(stop) / steps
@@ -195,6 +200,29 @@ def dominant_roofline(cfg, head):
     return line
 
 
+def fp8_error(work, device, rows=2):
+    """Error of the native FP8 mode against the reference numerics (the bf16
+    oracle) on `rows` sampled tokens of the workload's first routing."""
+    import torch
+
+    from glm_moe.layers.moe.routed_experts import routed_experts
+    from oracle import moe_oracle as O
+
+    x, ids, w = work.host[0]
+    xd, idd, wd = work.inputs[0]
+    out, _ = routed_experts(xd, idd, wd, *[work.tables[k] for k in TABLE_KEYS], activations="float8_e4m3fn")
+    got = out.float().cpu().numpy()
+    pick = np.random.default_rng(0).choice(x.shape[0], rows, replace=False)
+    used = np.unique(ids[pick].reshape(-1))
+    index = torch.as_tensor(used, dtype=torch.long, device=device)
+    host = {k: work.tables[k].index_select(0, index).cpu().numpy() for k in TABLE_KEYS}
+    remap = np.searchsorted(used, ids[pick]).astype(np.int32)
+    ref, _ = O.routed_experts(x[pick], remap, w[pick], **host)
+    err = np.abs(got[pick].astype(np.float64) - ref)
+    return {"max_abs": float(err.max()), "mean_rel": float(err.mean() / np.abs(ref).mean()),
+            "sample": f"{rows} tokens vs the bf16 oracle (reference numerics)"}
+
+
 def cpu_baseline(work, device):
     """The numpy oracle on this host's cores, on one layer of the same workload."""
     import torch
@@ -269,14 +297,20 @@ def main():
     for name in [s for s in args.secondary.split(",") if s]:
         if name == cfg.name:
             continue
-        scfg = S.CONFIGS[name]
+        base, _, mode = name.partition(":")
+        scfg = S.CONFIGS[base]
+        activations = "float8_e4m3fn" if mode == "fp8" else "bfloat16"
         print(f"[bench] secondary {name}", file=sys.stderr, flush=True)
-        swork = Workload(scfg, tables, device, rotations=8)
+        swork = Workload(scfg, tables, device, rotations=8, activations=activations)
         sms, _, _ = run_steps(swork, args.secondary_steps, 3, with_stage_events=False)
         _, sstages, sorder = run_steps(swork, args.secondary_steps, 3)
         s = summarize(swork, sms, sstages, sorder)
         s["hbm_frac"] = s["layer_hbm_gbs"] / HBM_PEAK_GBS
         s["bf16_mfma_frac"] = s["layer_tflops"] / BF16_PEAK_TFLOPS
+        if mode == "fp8":
+            s["activations"] = "float8_e4m3fn (native FP8 MFMA mode)"
+            s["fp8_mfma_frac"] = s["layer_tflops"] / FP8_PEAK_TFLOPS
+            s["error_vs_reference"] = fp8_error(swork, device)
         secondary[name] = s
         del swork
 

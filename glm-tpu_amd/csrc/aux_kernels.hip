@@ -117,6 +117,32 @@ __global__ void combine_routes_kernel(const uint16_t* y, int64_t tokens, int32_t
   }
 }
 
+// Activation quantisation of the native FP8 mode: one wave per (row, 128-wide
+// K block), two values a lane.  scale = amax / 448 (1 for an all-zero block);
+// q = e4m3fn(clamp(x / scale, +-448)) with round-to-nearest-even
+// (v_cvt_pk_fp8_f32); NaN stays NaN.
+__global__ __launch_bounds__(256) void quantize_rows_fp8_kernel(const uint16_t* x, int64_t rows, int64_t k,
+                                                                uint8_t* q, float* scales) {
+  const int lane = threadIdx.x & 63;
+  const int64_t kb = k / 128;
+  const int64_t blocks = rows * kb;
+  const int64_t waves = (int64_t)gridDim.x * (blockDim.x / 64);
+  for (int64_t blk = (int64_t)blockIdx.x * (blockDim.x / 64) + (threadIdx.x >> 6); blk < blocks; blk += waves) {
+    const int64_t row = blk / kb, col = (blk - row * kb) * 128 + 2 * lane;
+    const uint32_t pair = *reinterpret_cast<const uint32_t*>(x + row * k + col);
+    const float v0 = bf16_bits_to_f32(pair & 0xFFFFu), v1 = bf16_bits_to_f32(pair >> 16);
+    float m = fmaxf(fabsf(v0), fabsf(v1));
+#pragma unroll
+    for (int d = 32; d >= 1; d >>= 1) m = fmaxf(m, __shfl_xor(m, d, 64));
+    const float scale = m > 0.0f ? m / 448.0f : 1.0f;
+    auto clamp448 = [](float v) { return v != v ? v : fminf(fmaxf(v, -448.0f), 448.0f); };
+    const float a0 = clamp448(v0 / scale), a1 = clamp448(v1 / scale);
+    const uint32_t packed = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(a0, a1, 0, false);
+    *reinterpret_cast<uint16_t*>(q + row * k + col) = (uint16_t)(packed & 0xFFFFu);
+    if (lane == 0) scales[blk] = scale;
+  }
+}
+
 __global__ void fill_u32_kernel(uint32_t* dst, int64_t words, uint32_t value) {
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < words;
        i += (int64_t)gridDim.x * blockDim.x)
@@ -251,6 +277,16 @@ hipError_t launch_combine_routes(const uint16_t* y, int64_t tokens, int32_t top_
   if (total == 0) return hipSuccess;
   return launch_kernel(combine_routes_kernel, grid_for(total, 256), dim3(256), 0, stream, y, tokens,
                      top_k, h, ids, experts, bf16_sum, out);
+}
+
+hipError_t launch_quantize_rows_fp8(const uint16_t* x, int64_t rows, int64_t k, uint8_t* q, float* scales,
+                                    hipStream_t stream) {
+  if (rows <= 0 || k <= 0) return hipSuccess;
+  if (k % 128 != 0) return hipErrorInvalidValue;
+  const int64_t blocks = rows * (k / 128);
+  const int64_t wgs = (blocks + 3) / 4;
+  return launch_kernel(quantize_rows_fp8_kernel, dim3((unsigned)(wgs < 65536 ? wgs : 65536)), dim3(256), 0,
+                       stream, x, rows, k, q, scales);
 }
 
 hipError_t launch_fill_u32(void* dst, int64_t words, uint32_t value, hipStream_t stream) {

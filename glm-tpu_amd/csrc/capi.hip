@@ -74,9 +74,14 @@ int64_t max_tiles_for(int64_t routes, int32_t experts, int rows) {
   return (routes + rows - 1) / rows + (routes < experts ? routes : experts);
 }
 
+// Routed-expert calls of at most 64 routes take the two-kernel decode path.
+bool uses_decode_path(int64_t routes, int64_t hidden, int64_t intermediate) {
+  return routes <= kMaxDecodeRoutes && decode_path_fits(hidden, intermediate);
+}
+
 // Byte layout of the glm_moe_routed_experts workspace.
 struct RoutedLayout {
-  size_t sorted, inverse, counts, offsets, tiles, expert_tiles, act, y, total;
+  size_t sorted, inverse, counts, offsets, tiles, expert_tiles, act, y, xq, xscale, actq, actscale, total;
   int64_t max_tiles;
 };
 
@@ -95,6 +100,11 @@ RoutedLayout routed_layout(int64_t tokens, int32_t top_k, int32_t experts, int64
   L.expert_tiles = off; off = align_up(off + sizeof(int32_t) * 2 * experts);
   L.act = off;     off = align_up(off + sizeof(uint16_t) * n * intermediate);
   L.y = off;       off = align_up(off + sizeof(uint16_t) * n * hidden);
+  // native FP8 mode: quantised activations and their block scales
+  L.xq = off;       off = align_up(off + (size_t)tokens * hidden);
+  L.xscale = off;   off = align_up(off + sizeof(float) * tokens * (hidden / 128));
+  L.actq = off;     off = align_up(off + (size_t)n * intermediate);
+  L.actscale = off; off = align_up(off + sizeof(float) * n * (intermediate / 128));
   L.total = off;
   return L;
 }
@@ -153,6 +163,11 @@ int routed_experts_impl(const uint16_t* hidden, int64_t tokens, int64_t hidden_s
               "null tensor pointer");
   const int64_t n = tokens * top_k;
   const int shape = routed_shape(n, num_experts);
+  const bool fp8 = (flags & GLM_MOE_FP8_ACTIVATIONS) != 0;
+  GLM_REQUIRE(!fp8 || (!uses_decode_path(n, hidden_size, intermediate) && shape == kShapeWide &&
+                       prefill_fits(intermediate, hidden_size, 2) && prefill_fits(hidden_size, intermediate, 1)),
+              "FP8 activations need a prefill shape: more than 8 routes per expert on average, H and I multiples "
+              "of 512 (at most 8192), I a multiple of 128 rows per stripe");
   const int bn13 = gemm_shape_bn(shape, 2);
   const int bn2 = gemm_shape_bn(shape, 1);
   GLM_REQUIRE(intermediate % bn13 == 0, "intermediate size must be a multiple of %d", bn13);
@@ -174,9 +189,13 @@ int routed_experts_impl(const uint16_t* hidden, int64_t tokens, int64_t hidden_s
   int32_t* expert_tiles = expert_first_tile + num_experts;
   uint16_t* act = reinterpret_cast<uint16_t*>(ws + L.act);
   uint16_t* y = reinterpret_cast<uint16_t*>(ws + L.y);
+  uint8_t* xq = reinterpret_cast<uint8_t*>(ws + L.xq);
+  float* xscale = reinterpret_cast<float*>(ws + L.xscale);
+  uint8_t* actq = reinterpret_cast<uint8_t*>(ws + L.actq);
+  float* actscale = reinterpret_cast<float*>(ws + L.actscale);
 
   if (timer.events) *timer.timed = 0;
-  if (n <= kMaxDecodeRoutes && decode_path_fits(hidden_size, intermediate)) {
+  if (uses_decode_path(n, hidden_size, intermediate)) {
     // decode: two kernels that find their routes themselves and fuse the combine
     DecodeArgs d{};
     d.ids = route_indices;
@@ -252,6 +271,11 @@ int routed_experts_impl(const uint16_t* hidden, int64_t tokens, int64_t hidden_s
   g.max_tiles = (int32_t)L.max_tiles;
   g.expert_first_tile = expert_first_tile;
   g.expert_tiles = expert_tiles;
+  if (fp8) {
+    GLM_HIP(launch_quantize_rows_fp8(hidden, tokens, hidden_size, xq, xscale, stream), "quantize launch");
+    g.xq = xq;
+    g.xscale = xscale;
+  }
   g.valid = nullptr;
   g.out = act;
   g.ldo = intermediate;
@@ -281,6 +305,11 @@ int routed_experts_impl(const uint16_t* hidden, int64_t tokens, int64_t hidden_s
   d.max_tiles = (int32_t)L.max_tiles;
   d.expert_first_tile = expert_first_tile;
   d.expert_tiles = expert_tiles;
+  if (fp8) {
+    GLM_HIP(launch_quantize_rows_fp8(act, n, intermediate, actq, actscale, stream), "quantize launch");
+    d.xq = actq;
+    d.xscale = actscale;
+  }
   d.valid = nullptr;
   d.out = y;
   d.ldo = hidden_size;

@@ -321,6 +321,244 @@ __global__ __launch_bounds__(64 * WAVES, 1) void prefill_gemm_kernel(const Group
   }
 }
 
+// ---------------------------------------------------------------------------
+// Native FP8 mode: activations quantised per (row, 128-wide K block) to e4m3
+// with an FP32 scale (amax / 448), weights used as stored.  Per K block and
+// 16 x 16 output tile one v_mfma_scale_f32_16x16x128_f8f6f4 (unit E8M0 scales)
+// computes the e4m3 x e4m3 block product exactly in FP32, and the FP32 tile
+// accumulator takes it times (weight block scale x activation block scale).
+// Same work order, activation ring and weight transpose as the bf16 kernel;
+// no decode, half the activation bytes.
+typedef int i32x8 __attribute__((ext_vector_type(8)));
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ i32x8 join_i32x8(const u32x4& lo, const u32x4& hi) {
+  const i32x4 l = __builtin_bit_cast(i32x4, lo);
+  const i32x4 h = __builtin_bit_cast(i32x4, hi);
+  return __builtin_shufflevector(l, h, 0, 1, 2, 3, 4, 5, 6, 7);
+}
+
+template <int TABLES, int RG, int WAVES, int STAGES, int EPI>
+__global__ __launch_bounds__(64 * WAVES, 1) void prefill_gemm_fp8_kernel(const GroupedGemmArgs a) {
+  constexpr int BN = WAVES * RG * 16;
+  constexpr int ROWB = kScaleBlock;                          // e4m3 bytes of one activation row per K block
+  constexpr int STAGE = kBM * ROWB;                          // 16 KB
+  constexpr int XLOADS = STAGE / (WAVES * 1024);             // 1 KB activation loads per wave per K block
+  constexpr int WLOADS = TABLES * RG * 2;
+  constexpr int PER_BLOCK = XLOADS + 2 + WLOADS;             // + the two activation-scale loads
+  static_assert(XLOADS * WAVES * 1024 == STAGE, "activation stage split");
+  static_assert(STAGES % 2 == 0, "weight ring slots alternate");
+  constexpr int X_PENDING = (STAGES - 2) * PER_BLOCK;
+  extern __shared__ __attribute__((aligned(16))) uint8_t xs[];  // [STAGES][kBM][128 B], then weight transposes
+
+  if (a.valid != nullptr && a.valid[0] == 0) return;
+  const int stripes = a.n / BN;
+  const int total = stripes * a.tile_count[0];
+  const int per = (total + kXcds - 1) / kXcds;
+  const int b = blockIdx.x;
+  if (b / kXcds >= per) return;
+  const int item = (b % kXcds) * per + b / kXcds;
+  if (item >= total) return;
+  const int e = uniform(a.tile_expert[item / stripes]);
+  if (e < 0 || e >= a.experts) return;
+  const int t0 = uniform(a.expert_first_tile[e]);
+  const int nt = uniform(a.expert_tiles[e]);
+  if (nt <= 0) return;
+  const int rel = item - stripes * t0;
+  const int stripe = rel / nt;
+  const int tile = t0 + rel % nt;
+  if (stripe < 0 || stripe >= stripes || tile >= a.max_tiles) return;
+  const int r0 = uniform(a.tile_row[tile]);
+  const int live = uniform(a.tile_live[tile]);
+  if (uniform(a.tile_expert[tile]) != e || r0 < 0 || live <= 0 || live > kBM || r0 + live > a.rows) return;
+  const int ncg = (live + 15) >> 4;
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lrow = lane & 15;
+  const int lgrp = lane >> 4;
+  const int N = a.n;
+  const int K = a.k;
+  const int KB = K / kScaleBlock;
+  const int n0 = stripe * BN + wave * RG * 16;
+
+  auto phys_row = [&](int row) -> int64_t {
+    const int r = r0 + (row < live ? row : 0);  // padding rows repeat a live row; their columns are dropped
+    int64_t phys = a.x_row_ids ? a.x_row_ids[r] / a.x_row_div : r;
+    return phys < 0 ? 0 : (phys >= a.x_rows ? a.x_rows - 1 : phys);
+  };
+  // activations: instruction i covers rows 8 * (wave * XLOADS + i) + lane / 8,
+  // 128 bytes each; chunk c of row r lands in slot c ^ (r % 8)
+  const __amdgpu_buffer_rsrc_t xrsrc = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint8_t*>(a.xq), (short)0, (int)(a.x_rows * K), kBufferFormat);
+  int xoff[XLOADS];
+#pragma unroll
+  for (int i = 0; i < XLOADS; ++i) {
+    const int row = 8 * (wave * XLOADS + i) + (lane >> 3);
+    xoff[i] = (int)(phys_row(row) * K) + (((lane & 7) ^ (row & 7)) << 4);
+  }
+  // activation block scales: this lane fetches those of tile rows lane and lane + 64
+  const __amdgpu_buffer_rsrc_t srsrc = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<float*>(a.xscale), (short)0, (int)(a.x_rows * KB * 4), kBufferFormat);
+  int soff[2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) soff[h] = (int)(phys_row(lane + 64 * h) * KB * 4);
+
+  __amdgpu_buffer_rsrc_t wrsrc[TABLES][RG];
+  float sreg[TABLES][RG];
+  int woff[2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) woff[h] = (8 * h + (lane >> 3)) * K + (lane & 7) * 16;
+#pragma unroll
+  for (int t = 0; t < TABLES; ++t) {
+    const uint8_t* wb = t == 0 ? a.w0 : a.w1;
+    const float* sb = t == 0 ? a.s0 : a.s1;
+#pragma unroll
+    for (int rg = 0; rg < RG; ++rg) {
+      wrsrc[t][rg] = __builtin_amdgcn_make_buffer_rsrc(
+          const_cast<uint8_t*>(wb + ((size_t)e * N + n0 + rg * 16) * (size_t)K), (short)0, 16 * K, kBufferFormat);
+      const float* srow = sb + ((size_t)e * (N / kScaleBlock) + (n0 + rg * 16) / kScaleBlock) * KB;
+      sreg[t][rg] = lane < KB ? srow[lane] : 0.0f;
+    }
+  }
+
+  f32x4 acc[TABLES][RG][kCG];
+#pragma unroll
+  for (int t = 0; t < TABLES; ++t)
+#pragma unroll
+    for (int rg = 0; rg < RG; ++rg)
+#pragma unroll
+      for (int cg = 0; cg < kCG; ++cg) acc[t][rg][cg] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  u32x4 wring[2][TABLES][RG][2];
+  float sxr[STAGES][2];
+
+  auto issue = [&](int st, int kb, int kw) {
+    kb = kb < KB ? kb : KB - 1;
+    const int ws = kw & 1;
+    kw = kw < KB ? kw : KB - 1;
+    uint8_t* stage = xs + st * STAGE;
+#pragma unroll
+    for (int i = 0; i < XLOADS; ++i) load_lds_16(xrsrc, stage + (wave * XLOADS + i) * 1024, xoff[i], kb * ROWB);
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+      sxr[st][h] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(srsrc, soff[h], kb * 4, 0));
+#pragma unroll
+    for (int t = 0; t < TABLES; ++t)
+#pragma unroll
+      for (int rg = 0; rg < RG; ++rg)
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+          wring[ws][t][rg][h] = __builtin_bit_cast(
+              u32x4, __builtin_amdgcn_raw_buffer_load_b128(wrsrc[t][rg], woff[h], kw * kScaleBlock, kNonTemporal));
+  };
+
+  // weight ring slot -> this wave's LDS region -> MFMA A layout: lane l gets
+  // row l % 16, chunks 2 * (l / 16) and 2 * (l / 16) + 1 (32 e4m3 values)
+  uint8_t* wl = xs + STAGES * STAGE + wave * (TABLES * RG * 2048);
+  auto transpose = [&](int slot, u32x4 (&wt)[TABLES][RG][2]) {
+#pragma unroll
+    for (int t = 0; t < TABLES; ++t)
+#pragma unroll
+      for (int rg = 0; rg < RG; ++rg)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const int row = 8 * h + (lane >> 3);
+          *reinterpret_cast<u32x4*>(wl + (t * RG + rg) * 2048 + row * 128 + (((lane & 7) ^ (row & 7)) << 4)) =
+              wring[slot][t][rg][h];
+        }
+#pragma unroll
+    for (int t = 0; t < TABLES; ++t)
+#pragma unroll
+      for (int rg = 0; rg < RG; ++rg)
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+          wt[t][rg][h] = *reinterpret_cast<const u32x4*>(wl + (t * RG + rg) * 2048 + lrow * 128 +
+                                                          (((2 * lgrp + h) ^ (lrow & 7)) << 4));
+  };
+
+  auto run = [&](auto ncg_tag) {
+    constexpr int NCG = decltype(ncg_tag)::value;
+    auto step = [&](int st, const u32x4 (&wt)[TABLES][RG][2], int kb) {
+      const uint8_t* stage = xs + st * STAGE;
+      float sw[TABLES][RG];
+#pragma unroll
+      for (int t = 0; t < TABLES; ++t)
+#pragma unroll
+        for (int rg = 0; rg < RG; ++rg)
+          sw[t][rg] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, sreg[t][rg]), kb));
+#pragma unroll
+      for (int cg = 0; cg < NCG; ++cg) {
+        const int i = cg * 16 + lrow;
+        const uint8_t* rowp = stage + i * ROWB;
+        const u32x4 b0 = *reinterpret_cast<const u32x4*>(rowp + (((2 * lgrp) ^ (i & 7)) << 4));
+        const u32x4 b1 = *reinterpret_cast<const u32x4*>(rowp + (((2 * lgrp + 1) ^ (i & 7)) << 4));
+        const i32x8 bv = join_i32x8(b0, b1);
+        // scale of route column i: held by lane i % 64 of half i / 64
+        const float sx = __shfl(sxr[st][cg >> 2], (cg & 3) * 16 + lrow, 64);
+#pragma unroll
+        for (int t = 0; t < TABLES; ++t)
+#pragma unroll
+          for (int rg = 0; rg < RG; ++rg) {
+            const f32x4 p = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
+                join_i32x8(wt[t][rg][0], wt[t][rg][1]), bv, f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0, 127, 0, 127);
+            const float f = sw[t][rg] * sx;
+            f32x4 c = acc[t][rg][cg];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) c[j] = __builtin_fmaf(p[j], f, c[j]);
+            acc[t][rg][cg] = c;
+          }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    };
+#pragma unroll
+    for (int st = 0; st < STAGES - 1; ++st) issue(st, st, st < 2 ? st : 1);
+    for (int kb0 = 0; kb0 < KB; kb0 += STAGES) {
+#pragma unroll
+      for (int j = 0; j < STAGES; ++j) {
+        const int kb = kb0 + j;
+        wait_loads_then_barrier<X_PENDING>();
+        u32x4 wt[TABLES][RG][2];
+        transpose(j & 1, wt);  // weights of block kb leave their ring slot ...
+        issue((j + STAGES - 1) % STAGES, kb + STAGES - 1, kb + 2);  // ... which block kb + 2 refills
+        step(j, wt, kb);
+      }
+    }
+  };
+  if (ncg <= 2) run(std::integral_constant<int, 2>{});
+  else if (ncg <= 4) run(std::integral_constant<int, 4>{});
+  else if (ncg <= 6) run(std::integral_constant<int, 6>{});
+  else run(std::integral_constant<int, 8>{});
+  wait_all_loads();
+
+#pragma unroll
+  for (int cg = 0; cg < kCG; ++cg) {
+    const int col = cg * 16 + lrow;
+    if (cg >= ncg || col >= live) continue;
+#pragma unroll
+    for (int rg = 0; rg < RG; ++rg)
+      store_fragment<TABLES, EPI>(a, r0 + col, n0 + rg * 16 + lgrp * 4, acc[0][rg][cg], acc[TABLES - 1][rg][cg]);
+  }
+}
+
+template <int TABLES, int RG, int WAVES, int STAGES, int EPI>
+hipError_t launch_prefill_fp8(const GroupedGemmArgs& a, hipStream_t stream) {
+  constexpr int BN = WAVES * RG * 16;
+  const size_t lds = (size_t)STAGES * kBM * kScaleBlock + (size_t)WAVES * TABLES * RG * 2048;
+  static bool attr_set = false;
+  if (!attr_set) {
+    const hipError_t err = hipFuncSetAttribute(
+        reinterpret_cast<const void*>(prefill_gemm_fp8_kernel<TABLES, RG, WAVES, STAGES, EPI>),
+        hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (err != hipSuccess) return err;
+    attr_set = true;
+  }
+  const int64_t items = (int64_t)(a.n / BN) * a.max_tiles;
+  const int64_t grid = (items + kXcds - 1) / kXcds * kXcds;
+  return launch_kernel(prefill_gemm_fp8_kernel<TABLES, RG, WAVES, STAGES, EPI>, dim3((unsigned)grid),
+                       dim3(64 * WAVES), lds, stream, a);
+}
+
 template <int TABLES, int RG, int WAVES, int STAGES, int EPI>
 hipError_t launch_prefill(const GroupedGemmArgs& a, hipStream_t stream) {
   constexpr int BN = WAVES * RG * 16;
@@ -357,6 +595,14 @@ hipError_t launch_grouped_gemm_prefill(const GroupedGemmArgs& a, int tables, int
   if (a.max_tiles <= 0) return hipSuccess;
   if (a.expert_first_tile == nullptr || a.expert_tiles == nullptr) return hipErrorInvalidValue;
   if (!prefill_fits(a.n, a.k, tables)) return hipErrorInvalidValue;
+  if (a.xq != nullptr) {
+    if (a.xscale == nullptr) return hipErrorInvalidValue;
+    if (tables == 2 && epilogue == kEpiSwiglu)
+      return launch_prefill_fp8<2, 1, 8, kPrefillStages, kEpiSwiglu>(a, stream);
+    if (tables == 1 && epilogue == kEpiWeighted)
+      return launch_prefill_fp8<1, 2, 8, kPrefillStages, kEpiWeighted>(a, stream);
+    return hipErrorInvalidValue;
+  }
   if (tables == 2 && epilogue == kEpiSwiglu) return launch_prefill<2, 1, 8, kPrefillStages, kEpiSwiglu>(a, stream);
   if (tables == 1 && epilogue == kEpiWeighted) return launch_prefill<1, 2, 8, kPrefillStages, kEpiWeighted>(a, stream);
   return hipErrorInvalidValue;

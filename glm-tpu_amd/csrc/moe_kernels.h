@@ -116,6 +116,8 @@ struct GroupedGemmArgs {
   int32_t max_tiles;
   const int32_t* expert_first_tile;  // prefill kernel: first work-list tile of each expert
   const int32_t* expert_tiles;       // prefill kernel: work-list tiles of each expert
+  const uint8_t* xq;           // nullable: e4m3 activations [x_rows, k] for the native FP8 mode
+  const float* xscale;         // their FP32 block scales [x_rows, k / 128]
   const uint8_t* valid;        // nullable: no work at all when *valid == 0
   void* out;
   int64_t ldo;                 // elements between output rows
@@ -191,6 +193,10 @@ hipError_t launch_zero_rows(void* out, int64_t rows, int64_t row_bytes, const ui
 hipError_t launch_combine_routes(const uint16_t* y, int64_t tokens, int32_t top_k, int64_t h,
                                  const int32_t* ids, int32_t experts, int32_t bf16_sum,
                                  uint16_t* out, hipStream_t stream);
+// Per (row, 128-wide block): scale = amax / 448 (1 for an all-zero block),
+// q = e4m3fn(clamp(x / scale, +-448)) rounded to nearest even.
+hipError_t launch_quantize_rows_fp8(const uint16_t* x, int64_t rows, int64_t k, uint8_t* q, float* scales,
+                                    hipStream_t stream);
 hipError_t launch_fill_u32(void* dst, int64_t words, uint32_t value, hipStream_t stream);
 hipError_t launch_synth_fp8(uint64_t seed, int32_t experts, int64_t n, int64_t k, float sigma,
                             uint8_t* bits, float* scales, hipStream_t stream);

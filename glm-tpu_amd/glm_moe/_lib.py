@@ -25,6 +25,7 @@ BF16 = 1
 ROUTE_SUM_BF16 = 0x1
 CHECK_WEIGHTS = 0x2
 DROP_UNOWNED = 0x4
+FP8_ACTIVATIONS = 0x8
 
 _vp = ctypes.c_void_p
 _i32 = ctypes.c_int32

@@ -184,6 +184,7 @@ def routed_experts(
     route_sum: str = "float32",
     check_weights: bool = True,
     drop_unowned: bool = False,
+    activations: str = "bfloat16",
     out: torch.Tensor | None = None,
     events: StageEvents | None = None,
 ) -> tuple[torch.Tensor, torch.Tensor]:
@@ -193,6 +194,11 @@ def routed_experts(
     FP32 gate/up projections, bf16 SwiGLU, bf16 down projection, bf16 route
     weighting and the sum over the top-k slots (``route_sum``: FP32 with one
     rounding, or ``"bfloat16"`` for the decode body's bf16 sum, ``:293``).
+
+    ``activations="float8_e4m3fn"`` selects the native FP8 MFMA mode (no
+    reference counterpart; prefill shapes only): token rows and SwiGLU
+    activations are quantised per (row, 128-wide block) to e4m3 with an FP32
+    scale, and the e4m3 x e4m3 block products are scaled in FP32.
     """
     if hidden.ndim != 2 or hidden.dtype != torch.bfloat16:
         raise ValueError("routed experts take bf16 [tokens, hidden] rows")
@@ -214,6 +220,8 @@ def routed_experts(
             raise ValueError("expert scales must be float32 [E, N/128, K/128]")
     if route_sum not in ("float32", "bfloat16"):
         raise ValueError("route_sum must be float32 or bfloat16")
+    if activations not in ("bfloat16", "float8_e4m3fn"):
+        raise ValueError("activations must be bfloat16 or float8_e4m3fn")
     _lib.require_device(hidden, route_indices, route_weights, gate_bits, gate_scale, up_bits, up_scale,
                         down_bits, down_scale, out)
     device = hidden.device
@@ -230,6 +238,8 @@ def routed_experts(
         flags |= _lib.CHECK_WEIGHTS
     if drop_unowned:
         flags |= _lib.DROP_UNOWNED
+    if activations == "float8_e4m3fn":
+        flags |= _lib.FP8_ACTIVATIONS
     args = [
         _lib.ptr(hidden), tokens, h, _lib.ptr(route_indices), _lib.ptr(route_weights), top_k, experts, inter,
         _lib.ptr(gate_bits), _lib.ptr(gate_scale), _lib.ptr(up_bits), _lib.ptr(up_scale), _lib.ptr(down_bits),

@@ -47,6 +47,11 @@ enum glm_moe_dtype { GLM_MOE_F32 = 0, GLM_MOE_BF16 = 1 };
 #define GLM_MOE_ROUTE_SUM_BF16 0x1u   /* bf16 running route sum (decode body, routed_experts.py:293) */
 #define GLM_MOE_CHECK_WEIGHTS 0x2u    /* weights must be finite and >= 0 (prefill health, routed_experts.py:83) */
 #define GLM_MOE_DROP_UNOWNED 0x4u     /* routes with ids outside [0, E) contribute zero (decode ownership, routed_experts.py:250-253) */
+#define GLM_MOE_FP8_ACTIVATIONS 0x8u  /* native FP8 MFMA mode (no reference counterpart): activations quantised per
+                                         (row, 128-wide K block) to e4m3 with an FP32 scale amax/448, e4m3 x e4m3
+                                         block products, FP32 accumulation of product x weight scale x activation
+                                         scale.  Prefill shapes only (more than 8 routes per expert on average,
+                                         H/128 and I/128 multiples of 4, at most 64); others are refused. */
 
 int glm_moe_abi_version(void);
 const char* glm_moe_last_error(void);

@@ -332,6 +332,47 @@ def routed_projection(lhs, weights, local_expert_ids, owned, result_dtype: str =
     return _cast(out, result_dtype)
 
 
+# ----------------------------------------------------------------------------- native FP8 mode
+# The optional e4m3 x e4m3 mode of this library has no counterpart in the
+# reference: activations are quantised per (row, 128-wide K block) and the
+# block products are scaled in FP32.  These functions define it for its parity
+# test; its error against the reference numerics is reported separately.
+def quantize_rows_fp8(x) -> tuple[np.ndarray, np.ndarray]:
+    """``(e4m3 values as f32 [rows, K], f32 scales [rows, K/128])``.
+
+    scale = amax / 448 per block (1 for an all-zero block); q =
+    e4m3fn(clamp(x / scale, +-448)) rounded to nearest even (torch's
+    ``float8_e4m3fn`` cast, the independent decoder the table is pinned to).
+    """
+    import torch
+
+    x = np.asarray(x, np.float32)
+    rows, k = x.shape
+    blocks = x.reshape(rows, k // BLOCK, BLOCK)
+    amax = np.abs(blocks).max(axis=2)
+    scale = np.where(amax > 0, amax / np.float32(448.0), np.float32(1.0)).astype(np.float32)
+    v = np.clip(blocks / scale[:, :, None], np.float32(-448.0), np.float32(448.0)).astype(np.float32)
+    q = torch.from_numpy(np.ascontiguousarray(v)).to(torch.float8_e4m3fn).to(torch.float32).numpy()
+    return q.reshape(rows, k), scale
+
+
+def block_dot_fp8(xq, xscale, bits, wscale) -> np.ndarray:
+    """FP8-mode projection: per K block the exact e4m3 dot (FP64, one rounding to
+    FP32) times ``wscale[n/128, kb] * xscale[row, kb]``, accumulated in FP32 in
+    ascending K blocks.  ``bits`` are one expert's ``[N, K]`` e4m3 bytes."""
+    xq = np.asarray(xq, np.float64)
+    wq = _E4M3[np.asarray(bits, np.uint8)].astype(np.float64)
+    n, k = wq.shape
+    acc = np.zeros((xq.shape[0], n), np.float32)
+    for kb in range(k // BLOCK):
+        sl = slice(kb * BLOCK, (kb + 1) * BLOCK)
+        p = (xq[:, sl] @ wq[:, sl].T).astype(np.float32)
+        f = (np.repeat(np.asarray(wscale, np.float32)[:, kb], BLOCK)[None, :] *
+             np.asarray(xscale, np.float32)[:, kb : kb + 1]).astype(np.float32)
+        acc = (acc + p * f).astype(np.float32)
+    return acc
+
+
 def swiglu_bf16(gate_bf16, up_bf16) -> np.ndarray:
     """``(g * sigmoid(g) * u).astype(bf16)`` with a bf16 rounding after each op.
 
@@ -347,7 +388,7 @@ def swiglu_bf16(gate_bf16, up_bf16) -> np.ndarray:
 # ----------------------------------------------------------------------------- routed experts
 def routed_experts(hidden, route_indices, route_weights, gate_bits, gate_scale, up_bits, up_scale,
                    down_bits, down_scale, route_sum: str = "float32", check_weights: bool = True,
-                   drop_unowned: bool = False):
+                   drop_unowned: bool = False, activations: str = "bfloat16"):
     """The routed half of the MoE layer, returned as ``(bf16 [T, H] values, valid)``.
 
     ``prefill_moe_from_routes`` (``routed_experts.py:82-117``) on one device
@@ -366,6 +407,10 @@ def routed_experts(hidden, route_indices, route_weights, gate_bits, gate_scale, 
     on one device.
 
     Experts are decoded one at a time, so memory stays bounded at full shapes.
+
+    ``activations="float8_e4m3fn"`` is this library's native FP8 mode (no
+    reference counterpart): token rows and SwiGLU activations are quantised by
+    ``quantize_rows_fp8`` and every projection is ``block_dot_fp8``.
     """
     x = bf16_round(np.asarray(hidden, np.float32))
     ids = np.asarray(route_indices, np.int32)
@@ -381,16 +426,29 @@ def routed_experts(hidden, route_indices, route_weights, gate_bits, gate_scale, 
     offsets = np.concatenate([[0], np.cumsum(routes.group_sizes)])
     weighted = np.zeros((t * k, h), np.float32)  # flat (token, slot) order
     wr = bf16_round(w.reshape(-1))
+    if activations not in ("bfloat16", "float8_e4m3fn"):
+        raise ValueError("activations must be bfloat16 or float8_e4m3fn")
+    fp8 = activations == "float8_e4m3fn"
+    if fp8:
+        xq, xs = quantize_rows_fp8(x)
     for e in range(experts):
         r0, r1 = int(offsets[e]), int(offsets[e + 1])
         if r1 == r0:
             continue
         flat = sorted_ids[r0:r1]
-        rows = x[flat // k]
-        gate = bf16_round(block_dot_f32(rows, decode_fp8_table(gate_bits[e], gate_scale[e])))
-        up = bf16_round(block_dot_f32(rows, decode_fp8_table(up_bits[e], up_scale[e])))
-        act = swiglu_bf16(gate, up)
-        down = bf16_round(block_dot_f32(act, decode_fp8_table(down_bits[e], down_scale[e])))
+        if fp8:
+            tok = flat // k
+            gate = bf16_round(block_dot_fp8(xq[tok], xs[tok], gate_bits[e], gate_scale[e]))
+            up = bf16_round(block_dot_fp8(xq[tok], xs[tok], up_bits[e], up_scale[e]))
+            act = swiglu_bf16(gate, up)
+            aq, ascale = quantize_rows_fp8(act)
+            down = bf16_round(block_dot_fp8(aq, ascale, down_bits[e], down_scale[e]))
+        else:
+            rows = x[flat // k]
+            gate = bf16_round(block_dot_f32(rows, decode_fp8_table(gate_bits[e], gate_scale[e])))
+            up = bf16_round(block_dot_f32(rows, decode_fp8_table(up_bits[e], up_scale[e])))
+            act = swiglu_bf16(gate, up)
+            down = bf16_round(block_dot_f32(act, decode_fp8_table(down_bits[e], down_scale[e])))
         weighted[flat] = bf16_round(down * wr[flat][:, None])
     if drop_unowned:
         owned = ((ids >= 0) & (ids < experts)).reshape(-1)

@@ -433,3 +433,53 @@ def test_prefill_production_shape_sampled_tokens(device, production_tables, name
     print(name, assert_moe_close(full[rows], ref))
     again, _ = routed_experts(*args)
     np.testing.assert_array_equal(bf16_bits_of(again), bf16_bits_of(out))
+
+
+# ----------------------------------------------------------------------------- native FP8 mode
+# No reference counterpart: the mode is checked against its own definition in
+# the oracle (quantize_rows_fp8 / block_dot_fp8) to the north-star tolerance,
+# and its error against the reference numerics (the bf16 oracle) is reported.
+FP8_ERROR_BOUND = 5e-2  # mean-rel against the bf16 reference numerics (e4m3 activations: 3 mantissa bits)
+
+
+def test_fp8_mode_matches_its_oracle_and_reports_its_error(device):
+    from glm_moe.layers.moe.routed_experts import routed_experts
+
+    cfg, x, ids, w, tables = _small_case(512, 16, 512, 512, 8, 0.0, seed=77)
+    t = _device_tables(tables, device)
+    args = (bf16_dev(x, device), dev(ids, device), dev(w, device), *(t[k] for k in TABLE_KEYS))
+    out, ok = routed_experts(*args, activations="float8_e4m3fn")
+    assert bool(ok)
+    got = host_f32(out)
+    ref8, _ = O.routed_experts(x, ids, w, **tables, activations="float8_e4m3fn")
+    print("fp8 mode vs fp8 oracle:", assert_moe_close(got, ref8))
+    ref16, _ = O.routed_experts(x, ids, w, **tables)
+    err = np.abs(got - ref16)
+    rel = err.mean() / np.abs(ref16).mean()
+    print(f"fp8 mode vs reference numerics: max-abs {err.max():.3e}, mean-rel {rel:.3e}")
+    assert rel <= FP8_ERROR_BOUND
+    again, _ = routed_experts(*args, activations="float8_e4m3fn")
+    np.testing.assert_array_equal(bf16_bits_of(again), bf16_bits_of(out))  # deterministic
+
+
+def test_fp8_mode_production_shape_sampled_tokens(device, production_tables):
+    from glm_moe import synthetic as S
+    from glm_moe.layers.moe.routed_experts import routed_experts
+
+    cfg = S.CONFIGS["prefill_t2048"]
+    x = S.hidden_states(cfg, 7)
+    ids, w = S.routes(cfg, 7)
+    t = production_tables
+    out, ok = routed_experts(bf16_dev(x, device), dev(ids, device), dev(w, device), *(t[k] for k in TABLE_KEYS),
+                             activations="float8_e4m3fn")
+    assert bool(ok)
+    full = host_f32(out)
+    assert np.all(np.isfinite(full))
+    rows = np.random.default_rng(1).choice(cfg.tokens, 4, replace=False)
+    host, local_ids = _subproblem(t, ids[rows])
+    ref8, _ = O.routed_experts(x[rows], local_ids, w[rows], **host, activations="float8_e4m3fn")
+    print("prefill_t2048 fp8 mode vs fp8 oracle:", assert_moe_close(full[rows], ref8))
+    ref16, _ = O.routed_experts(x[rows], local_ids, w[rows], **host)
+    err = np.abs(full[rows] - ref16)
+    print(f"prefill_t2048 fp8 mode vs reference numerics: max-abs {err.max():.3e}, "
+          f"mean-rel {err.mean() / np.abs(ref16).mean():.3e}")

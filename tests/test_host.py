@@ -91,6 +91,13 @@ def test_static_refusals_raise_value_error_through_the_abi():
     status = lib.glm_moe_routed_experts(null, 1, 6144, null, null, 8, 256, 2048, null, null, null, null, null,
                                         null, 0, null, null, null, 0, null)
     assert status == _lib.ERR_ARGUMENT  # null tensors refused before any launch
+    # the native FP8 mode is refused on decode shapes, before any device work
+    fake = ctypes.c_void_p(256)
+    status = lib.glm_moe_routed_experts(fake, 1, 6144, fake, fake, 8, 256, 2048, fake, fake, fake, fake, fake,
+                                        fake, _lib.FP8_ACTIVATIONS, fake, fake, fake, 1 << 30, null)
+    assert status == _lib.ERR_ARGUMENT
+    with pytest.raises(ValueError, match="FP8 activations need a prefill shape"):
+        _lib.check(status)
 
 
 def test_python_api_refuses_bad_geometry_and_cpu_tensors():

@@ -342,3 +342,43 @@ def test_synthetic_router_agrees_with_oracle_router():
         b = O.route_glm_noaux_tc_logits(logits, np.zeros(cfg.experts, np.float32), cfg.top_k)
         np.testing.assert_array_equal(a[0], b[0])
         np.testing.assert_array_equal(a[1], b[1])
+
+
+# ----------------------------------------------------------------------------- native FP8 mode (no reference counterpart)
+def test_fp8_activation_quantization_known_answers():
+    # block 0: amax 448 -> scale 1, values already on the e4m3 grid stay exact;
+    # block 1: all zero -> scale 1, zeros; block 2: amax 2 -> scale 2/448, its
+    # largest value maps to exactly 448 and the rest round to nearest even
+    x = np.zeros((1, 3 * 128), np.float32)
+    grid = O.fp8_e4m3fn_table()[np.arange(0, 127, dtype=np.uint8)]  # positive finite codes 0..126
+    x[0, :127] = grid
+    x[0, 127] = -448.0
+    x[0, 256] = 2.0
+    x[0, 257] = -1.0
+    x[0, 258] = 2.0 * 17.0 / 448.0  # 17 lies between e4m3 16 and 18: a tie, rounds to even (16)
+    q, s = O.quantize_rows_fp8(x)
+    np.testing.assert_array_equal(s[0], np.float32([1.0, 1.0, 2.0 / 448.0]))
+    np.testing.assert_array_equal(q[0, :127], grid)
+    assert q[0, 127] == -448.0
+    assert not np.any(q[0, 128:256])
+    assert q[0, 256] == 448.0 and q[0, 257] == -224.0 and q[0, 258] == 16.0
+
+
+def test_block_dot_fp8_is_exact_block_products_times_scales():
+    rng = np.random.default_rng(5)
+    bits = rng.integers(0, 126, (256, 256), dtype=np.uint8)  # finite codes only
+    bits[bits == 0x7F] = 0
+    wscale = rng.uniform(0.5, 2.0, (2, 2)).astype(np.float32)
+    x = rng.standard_normal((3, 256)).astype(np.float32)
+    xq, xs = O.quantize_rows_fp8(x)
+    got = O.block_dot_fp8(xq, xs, bits, wscale)
+    # closed form in FP64: sum over blocks of (exact block dot) * w scale * x scale
+    w = O.fp8_e4m3fn_table()[bits].astype(np.float64)
+    ref = np.zeros((3, 256))
+    for kb in range(2):
+        sl = slice(128 * kb, 128 * kb + 128)
+        ref += (xq[:, sl].astype(np.float64) @ w[:, sl].T) * np.repeat(wscale[:, kb], 128)[None, :] * xs[:, kb:kb + 1]
+    np.testing.assert_allclose(got, ref, rtol=1e-5, atol=1e-5)
+    # and it approximates the dequantised FP32 product to e4m3 precision
+    dense = x @ (O.fp8_e4m3fn_table()[bits] * np.repeat(np.repeat(wscale, 128, 0), 128, 1)).T
+    assert np.abs(got - dense).max() < 0.1 * np.abs(dense).max()
