@@ -21,11 +21,11 @@
 //   * One workgroup barrier per K block; when it is passed, the block's rows
 //     are in LDS and every wave has finished with the block STAGES - 1 back,
 //     whose slot is refilled next.
-// Work items are ordered expert-major, then stripe, then route tile, and
-// laid out XCD-aware: workgroup b runs on XCD b % 8, and XCD x walks the
-// contiguous range [x * per, (x + 1) * per) of work items, so the tiles that
-// share an expert's weight stripe (hot experts) or the stripes that share a
-// tile's activation rows run together on one XCD and meet in its L2.
+// Work items are ordered expert-major, then in blocks of route tiles x
+// stripes (item_of_expert), and laid out XCD-aware: workgroup b runs on XCD
+// b % 8, and XCD x walks the contiguous range [x * per, (x + 1) * per) of work
+// items, so the tiles that share an expert's weight stripe (hot experts) and
+// the stripes that share a tile's activation rows run together on one XCD.
 #include <type_traits>
 
 #include "gemm_epilogue.h"
@@ -53,6 +53,23 @@ constexpr int kStageBytes = kBM * kRowBytes; // 32 KB
 // outstanding load, so the weight and activation prefetches of later K blocks
 // stay in flight across the barrier.  Inline asm with a memory clobber: the
 // compiler moves no memory access across it.
+// Work items of one expert (stripes x nt route tiles), in the order an XCD
+// walks them: tile blocks of kTileBlock tiles, each over every stripe, each
+// stripe over the block's tiles.  Consecutive items -- the ones an XCD's CUs
+// run together -- then share kTileBlock activation tiles and ~32 / kTileBlock
+// weight stripes.  An expert with one tile (uniform prefill) walks its
+// stripes over the same activation rows.
+constexpr int kTileBlock = 4;
+
+__device__ __forceinline__ void item_of_expert(int rel, int stripes, int nt, int& stripe, int& tile) {
+  const int tb = rel / (stripes * kTileBlock);
+  const int first = tb * kTileBlock;
+  const int bs = min(kTileBlock, nt - first);
+  const int r = rel - tb * stripes * kTileBlock;
+  stripe = r / bs;
+  tile = first + r % bs;
+}
+
 template <int N>
 __device__ __forceinline__ void wait_loads_then_barrier() {
   static_assert(N >= 0 && N < 64, "vmcnt range");
@@ -100,9 +117,9 @@ __global__ __launch_bounds__(64 * WAVES, 1) void prefill_gemm_kernel(const Group
   const int t0 = uniform(a.expert_first_tile[e]);
   const int nt = uniform(a.expert_tiles[e]);
   if (nt <= 0) return;
-  const int rel = item - stripes * t0;
-  const int stripe = rel / nt;
-  const int tile = t0 + rel % nt;
+  int stripe, tile;
+  item_of_expert(item - stripes * t0, stripes, nt, stripe, tile);
+  tile += t0;
   if (stripe < 0 || stripe >= stripes || tile >= a.max_tiles) return;
   const int r0 = uniform(a.tile_row[tile]);
   const int live = uniform(a.tile_live[tile]);
@@ -364,9 +381,9 @@ __global__ __launch_bounds__(64 * WAVES, 1) void prefill_gemm_fp8_kernel(const G
   const int t0 = uniform(a.expert_first_tile[e]);
   const int nt = uniform(a.expert_tiles[e]);
   if (nt <= 0) return;
-  const int rel = item - stripes * t0;
-  const int stripe = rel / nt;
-  const int tile = t0 + rel % nt;
+  int stripe, tile;
+  item_of_expert(item - stripes * t0, stripes, nt, stripe, tile);
+  tile += t0;
   if (stripe < 0 || stripe >= stripes || tile >= a.max_tiles) return;
   const int r0 = uniform(a.tile_row[tile]);
   const int live = uniform(a.tile_live[tile]);
