@@ -81,7 +81,8 @@ bool uses_decode_path(int64_t routes, int64_t hidden, int64_t intermediate) {
 
 // Byte layout of the glm_moe_routed_experts workspace.
 struct RoutedLayout {
-  size_t sorted, inverse, counts, offsets, tiles, expert_tiles, act, y, xq, xscale, actq, actscale, total;
+  size_t sorted, inverse, counts, offsets, tiles, expert_tiles, chunk_hist, chunk_bad, act, y, xq, xscale, actq,
+      actscale, total;
   int64_t max_tiles;
 };
 
@@ -98,6 +99,9 @@ RoutedLayout routed_layout(int64_t tokens, int32_t top_k, int32_t experts, int64
   L.offsets = off; off = align_up(off + sizeof(int32_t) * (experts + 1));
   L.tiles = off;   off = align_up(off + sizeof(int32_t) * (3 * L.max_tiles + 1));
   L.expert_tiles = off; off = align_up(off + sizeof(int32_t) * 2 * experts);
+  const int chunks = route_plan_chunks((int32_t)n, top_k);
+  L.chunk_hist = off; off = align_up(off + sizeof(int32_t) * (size_t)chunks * experts);
+  L.chunk_bad = off;  off = align_up(off + sizeof(int32_t) * (size_t)chunks);
   L.act = off;     off = align_up(off + sizeof(uint16_t) * n * intermediate);
   L.y = off;       off = align_up(off + sizeof(uint16_t) * n * hidden);
   // native FP8 mode: quantised activations and their block scales
@@ -244,6 +248,8 @@ int routed_experts_impl(const uint16_t* hidden, int64_t tokens, int64_t hidden_s
   p.tile_count = tile_count;
   p.expert_first_tile = expert_first_tile;
   p.expert_tiles = expert_tiles;
+  p.chunk_hist = reinterpret_cast<int32_t*>(ws + L.chunk_hist);
+  p.chunk_bad = reinterpret_cast<int32_t*>(ws + L.chunk_bad);
   timer.arm(kStagePlan);
   GLM_HIP(launch_route_plan(p, stream), "route plan launch");
   timer.done(kStagePlan);
@@ -350,7 +356,7 @@ int glm_moe_decode_fp8_table(const uint8_t* bits, const float* scale, int64_t n,
 int glm_moe_group_routes(const int32_t* route_indices, int64_t tokens, int32_t top_k,
                          int32_t num_experts, int32_t* sorted_flat_ids,
                          int32_t* inverse_permutation, int32_t* group_sizes, uint8_t* valid,
-                         void* stream) {
+                         void* workspace, size_t workspace_bytes, void* stream) {
   GLM_REQUIRE(tokens > 0 && top_k > 0, "routes must be nonempty [tokens,top_k]");
   GLM_REQUIRE(num_experts > 0, "num_experts must be a positive integer");
   GLM_REQUIRE(top_k <= num_experts, "top_k exceeds expert count");
@@ -368,8 +374,20 @@ int glm_moe_group_routes(const int32_t* route_indices, int64_t tokens, int32_t t
   p.inverse = inverse_permutation;
   p.counts = group_sizes;
   p.valid = valid;
+  if (workspace != nullptr &&
+      workspace_bytes >= glm_moe_group_routes_workspace_bytes(tokens, top_k, num_experts)) {
+    const int chunks = route_plan_chunks(p.n, top_k);
+    p.chunk_hist = static_cast<int32_t*>(workspace);
+    p.chunk_bad = p.chunk_hist + (size_t)chunks * num_experts;
+  }
   GLM_HIP(launch_route_plan(p, as_stream(stream)), "route plan launch");
   return GLM_MOE_OK;
+}
+
+size_t glm_moe_group_routes_workspace_bytes(int64_t tokens, int32_t top_k, int32_t num_experts) {
+  if (tokens <= 0 || top_k <= 0 || num_experts <= 0 || tokens * top_k > INT32_MAX / 2) return 0;
+  const size_t chunks = (size_t)route_plan_chunks((int32_t)(tokens * top_k), top_k);
+  return sizeof(int32_t) * chunks * ((size_t)num_experts + 1);
 }
 
 int glm_moe_gather_rows(const void* src, int64_t src_rows, int64_t row_bytes,

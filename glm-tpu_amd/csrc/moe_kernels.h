@@ -61,7 +61,14 @@ struct RoutePlanArgs {
   int32_t* tile_count;       // [1]
   int32_t* expert_first_tile;  // nullable [experts]: first tile of each expert
   int32_t* expert_tiles;       // nullable [experts]: tiles of each expert
+  // optional scratch for the multi-workgroup plan (route_plan_chunks() chunks):
+  int32_t* chunk_hist;         // [chunks, experts] expert counts of each chunk
+  int32_t* chunk_bad;          // [chunks] health of each chunk
+  int32_t chunk;               // routes per chunk (set by launch_route_plan)
 };
+// Route chunks of the multi-workgroup plan (whole token rows, about 2048 routes each).
+constexpr int kPlanChunkRoutes = 2048;
+int route_plan_chunks(int32_t n, int32_t top_k);
 hipError_t launch_route_plan(const RoutePlanArgs& a, hipStream_t stream);
 
 struct PanelPlanArgs {

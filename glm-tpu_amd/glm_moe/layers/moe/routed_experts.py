@@ -62,10 +62,12 @@ def group_prefill_routes(route_indices: torch.Tensor, *, num_experts: int = 256)
     inverse = torch.empty(n, dtype=torch.int32, device=device)
     counts = torch.empty(num_experts, dtype=torch.int32, device=device)
     valid = torch.empty((), dtype=torch.bool, device=device)
+    scratch_bytes = int(_lib.lib().glm_moe_group_routes_workspace_bytes(tokens, top_k, num_experts))
+    scratch = torch.empty(max(scratch_bytes, 1), dtype=torch.uint8, device=device)
     _lib.call(
         "glm_moe_group_routes",
         _lib.ptr(route_indices), tokens, top_k, num_experts, _lib.ptr(order), _lib.ptr(inverse),
-        _lib.ptr(counts), _lib.ptr(valid), _lib.stream_of(route_indices),
+        _lib.ptr(counts), _lib.ptr(valid), _lib.ptr(scratch), scratch.numel(), _lib.stream_of(route_indices),
     )
     return PrefillRoutes(order, inverse, counts, valid)
 

@@ -70,7 +70,11 @@ int glm_moe_decode_fp8_table(const uint8_t* bits, const float* scale, int64_t n,
 int glm_moe_group_routes(const int32_t* route_indices, int64_t tokens, int32_t top_k,
                          int32_t num_experts, int32_t* sorted_flat_ids,
                          int32_t* inverse_permutation, int32_t* group_sizes, uint8_t* valid,
-                         void* stream);
+                         void* workspace, size_t workspace_bytes, void* stream);
+/* Optional scratch of glm_moe_group_routes: with at least this many bytes of
+ * workspace, large route sets are grouped by many workgroups (same result);
+ * with NULL / too few bytes, by one. */
+size_t glm_moe_group_routes_workspace_bytes(int64_t tokens, int32_t top_k, int32_t num_experts);
 
 /* Replaces glm_tpu/layers/moe/routed_experts.py:167-183 gather_prefill_route_rows /
  * restore_prefill_route_rows and panels.py:98-104 unpack_expert_panel_rows:

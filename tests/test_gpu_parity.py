@@ -113,6 +113,24 @@ def test_group_routes_zipf_8192_is_bit_exact(device, seed):
     assert int(ref.group_sizes.max()) > 1000  # the skew the config asks for
 
 
+@pytest.mark.parametrize("top_k,rows,invalid", [(6, 700, False), (8, 1000, True), (5, 3000, False)])
+def test_group_routes_many_chunks_is_bit_exact(device, top_k, rows, invalid):
+    """Route sets of several 2048-route chunks (whole rows: a chunk of 6-wide rows
+    holds 2046 routes), with and without an invalid id in a late chunk."""
+    from glm_moe.layers.moe.routed_experts import group_prefill_routes
+
+    rng = np.random.default_rng(top_k * rows)
+    ids = np.stack([rng.choice(64, top_k, replace=False) for _ in range(rows)]).astype(np.int32)
+    if invalid:
+        ids[rows - 3, 1] = 64
+    got = group_prefill_routes(dev(ids, device), num_experts=64)
+    ref = O.group_prefill_routes(ids, num_experts=64)
+    np.testing.assert_array_equal(got.sorted_flat_ids.cpu().numpy(), ref.sorted_flat_ids)
+    np.testing.assert_array_equal(got.inverse_permutation.cpu().numpy(), ref.inverse_permutation)
+    np.testing.assert_array_equal(got.group_sizes.cpu().numpy(), ref.group_sizes)
+    assert bool(got.valid) == bool(ref.valid) == (not invalid)
+
+
 @pytest.mark.parametrize("bad", [-1, 256, 0, 2**31 - 1])
 def test_group_routes_invalid_ids_match_reference_metadata(device, bad):
     from glm_moe.layers.moe.routed_experts import group_prefill_routes

@@ -83,8 +83,8 @@ def test_static_refusals_raise_value_error_through_the_abi():
     assert status == _lib.ERR_ARGUMENT
     with pytest.raises(ValueError, match="M32/N256/K128"):
         _lib.check(status)
-    assert lib.glm_moe_group_routes(null, 0, 8, 256, null, null, null, null, null) == _lib.ERR_ARGUMENT
-    assert lib.glm_moe_group_routes(null, 2, 9, 8, null, null, null, null, null) == _lib.ERR_ARGUMENT
+    assert lib.glm_moe_group_routes(null, 0, 8, 256, null, null, null, null, null, 0, null) == _lib.ERR_ARGUMENT
+    assert lib.glm_moe_group_routes(null, 2, 9, 8, null, null, null, null, null, 0, null) == _lib.ERR_ARGUMENT
     status = lib.glm_moe_routed_projection(null, 8, 6144, 3, null, null, null, null, 256, 2048, null, null, 0,
                                            null, null, 0, null)
     assert status == _lib.ERR_ARGUMENT
