@@ -117,6 +117,72 @@ __global__ void combine_routes_kernel(const uint16_t* y, int64_t tokens, int32_t
   }
 }
 
+// GLM noaux_tc routing (reference glm_tpu/layers/moe/router.py:20-55), one
+// wave per token: scores = FP32 sigmoid(logits); the top_k experts of
+// scores + bias, best first, ties to the lowest id (lax.top_k's order);
+// weights = the chosen unbiased scores over their FP32 sum (summed in
+// selection order).  Each lane holds experts lane, lane + 64, ... (E <= 1024).
+__global__ __launch_bounds__(256) void route_noaux_tc_kernel(const float* logits, int64_t tokens, int32_t experts,
+                                                             const float* bias, int32_t top_k, int32_t* ids,
+                                                             float* weights) {
+  constexpr int kPer = kMaxExperts / 64;
+  const int lane = threadIdx.x & 63;
+  const int64_t t = (int64_t)blockIdx.x * (blockDim.x / 64) + (threadIdx.x >> 6);
+  if (t >= tokens) return;
+  float score[kPer], biased[kPer];
+#pragma unroll
+  for (int j = 0; j < kPer; ++j) {
+    const int e = lane + 64 * j;
+    const bool live = e < experts;
+    const float x = live ? logits[t * experts + e] : 0.0f;
+    score[j] = sigmoid_f32(x);
+    biased[j] = live ? score[j] + (bias ? bias[e] : 0.0f) : -INFINITY;
+  }
+  // round r's winner is wave-uniform: lane r keeps it; the sum runs in selection order
+  int my_id = 0;
+  float my_score = 0.0f, sum = 0.0f;
+  for (int r = 0; r < top_k; ++r) {
+    // this lane's best remaining (highest biased score, then lowest id)
+    float bv = -INFINITY;
+    int be = 0x7fffffff;
+    float bs = 0.0f;
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+      const int e = lane + 64 * j;
+      if (e < experts && (biased[j] > bv || (biased[j] == bv && e < be))) {
+        bv = biased[j];
+        be = e;
+        bs = score[j];
+      }
+    }
+    // wave arg-max with the same order
+#pragma unroll
+    for (int d = 32; d >= 1; d >>= 1) {
+      const float ov = __shfl_xor(bv, d, 64);
+      const int oe = __shfl_xor(be, d, 64);
+      const float os = __shfl_xor(bs, d, 64);
+      if (ov > bv || (ov == bv && oe < be)) {
+        bv = ov;
+        be = oe;
+        bs = os;
+      }
+    }
+    if (lane == r) {
+      my_id = be;
+      my_score = bs;
+    }
+    sum += bs;
+    // remove the winner from its owner lane
+#pragma unroll
+    for (int j = 0; j < kPer; ++j)
+      if (lane + 64 * j == be) biased[j] = -INFINITY;
+  }
+  if (lane < top_k) {
+    ids[t * top_k + lane] = my_id;
+    weights[t * top_k + lane] = my_score / sum;
+  }
+}
+
 // Activation quantisation of the native FP8 mode: one wave per (row, 128-wide
 // K block), two values a lane.  scale = amax / 448 (1 for an all-zero block);
 // q = e4m3fn(clamp(x / scale, +-448)) with round-to-nearest-even
@@ -277,6 +343,16 @@ hipError_t launch_combine_routes(const uint16_t* y, int64_t tokens, int32_t top_
   if (total == 0) return hipSuccess;
   return launch_kernel(combine_routes_kernel, grid_for(total, 256), dim3(256), 0, stream, y, tokens,
                      top_k, h, ids, experts, bf16_sum, out);
+}
+
+hipError_t launch_route_noaux_tc(const float* logits, int64_t tokens, int32_t experts, const float* bias,
+                                 int32_t top_k, int32_t* ids, float* weights, hipStream_t stream) {
+  if (tokens <= 0) return hipSuccess;
+  if (experts <= 0 || experts > kMaxExperts || top_k <= 0 || top_k > 16 || top_k > experts)
+    return hipErrorInvalidValue;
+  const int64_t blocks = (tokens + 3) / 4;
+  return launch_kernel(route_noaux_tc_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, logits, tokens,
+                       experts, bias, top_k, ids, weights);
 }
 
 hipError_t launch_quantize_rows_fp8(const uint16_t* x, int64_t rows, int64_t k, uint8_t* q, float* scales,

@@ -353,6 +353,20 @@ int glm_moe_decode_fp8_table(const uint8_t* bits, const float* scale, int64_t n,
   return GLM_MOE_OK;
 }
 
+int glm_moe_route_noaux_tc(const float* router_logits, int64_t tokens, int32_t num_experts,
+                           const float* correction_bias, int32_t top_k, int32_t* route_indices,
+                           float* route_weights, void* stream) {
+  GLM_REQUIRE(tokens >= 0, "router_logits must have shape [tokens, experts]");
+  GLM_REQUIRE(num_experts > 0 && num_experts <= kMaxExperts, "at most %d experts", kMaxExperts);
+  GLM_REQUIRE(top_k > 0 && top_k <= num_experts && top_k <= 16, "top_k must be in [1, num_experts] (at most 16)");
+  if (tokens == 0) return GLM_MOE_OK;
+  GLM_REQUIRE(router_logits && route_indices && route_weights, "null tensor pointer");
+  GLM_HIP(launch_route_noaux_tc(router_logits, tokens, num_experts, correction_bias, top_k, route_indices,
+                                route_weights, as_stream(stream)),
+          "router launch");
+  return GLM_MOE_OK;
+}
+
 int glm_moe_group_routes(const int32_t* route_indices, int64_t tokens, int32_t top_k,
                          int32_t num_experts, int32_t* sorted_flat_ids,
                          int32_t* inverse_permutation, int32_t* group_sizes, uint8_t* valid,

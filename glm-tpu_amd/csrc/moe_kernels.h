@@ -200,6 +200,9 @@ hipError_t launch_zero_rows(void* out, int64_t rows, int64_t row_bytes, const ui
 hipError_t launch_combine_routes(const uint16_t* y, int64_t tokens, int32_t top_k, int64_t h,
                                  const int32_t* ids, int32_t experts, int32_t bf16_sum,
                                  uint16_t* out, hipStream_t stream);
+// GLM noaux_tc routing of [tokens, experts] FP32 logits (experts <= 1024, top_k <= 16).
+hipError_t launch_route_noaux_tc(const float* logits, int64_t tokens, int32_t experts, const float* bias,
+                                 int32_t top_k, int32_t* ids, float* weights, hipStream_t stream);
 // Per (row, 128-wide block): scale = amax / 448 (1 for an all-zero block),
 // q = e4m3fn(clamp(x / scale, +-448)) rounded to nearest even.
 hipError_t launch_quantize_rows_fp8(const uint16_t* x, int64_t rows, int64_t k, uint8_t* q, float* scales,

@@ -9,6 +9,7 @@ from glm_moe.layers.moe.routed_experts import (
     restore_prefill_route_rows,
     routed_experts,
 )
+from glm_moe.layers.moe.router import route_glm_noaux_tc_logits
 
 __all__ = [
     "PrefillRoutes",
@@ -17,5 +18,6 @@ __all__ = [
     "moe_grouped_routes",
     "prefill_moe_from_routes",
     "restore_prefill_route_rows",
+    "route_glm_noaux_tc_logits",
     "routed_experts",
 ]

@@ -1,0 +1,50 @@
+"""The MoE router's expert selection on the GPU (libglm_moe).
+
+Mirrors ``route_glm_noaux_tc_logits`` of ``glm_tpu/layers/moe/router.py:20-55``:
+FP32 sigmoid scores; the correction bias takes part in the selection only; the
+top-k of the biased scores, best first, ties to the lowest expert id
+(``lax.top_k``'s order); the weights are the chosen unbiased scores normalised
+by their FP32 sum.  Routed scaling is not applied here (the reference applies it
+to the reduced routed output).
+"""
+
+from __future__ import annotations
+
+from collections.abc import Callable
+from typing import Any
+
+import torch
+
+from glm_moe import _lib
+
+
+def route_glm_noaux_tc_logits(
+    router_logits: torch.Tensor,
+    correction_bias: torch.Tensor,
+    *,
+    top_k: int = 8,
+    _observe: Callable[[str, dict[str, Any]], None] | None = None,
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """Return selected expert ids (int32 ``[T, k]``) and normalised sigmoid weights (f32).
+
+    ``_observe`` receives the selection (indices and weights) under the
+    reference's event name; the intermediate score tensors stay on the device
+    kernel and are not materialised.
+    """
+    if router_logits.ndim != 2:
+        raise ValueError("router_logits must have shape [tokens, experts]")
+    tokens, experts = router_logits.shape
+    if tuple(correction_bias.shape) != (experts,):
+        raise ValueError(f"correction_bias must have shape {(experts,)}, got {tuple(correction_bias.shape)}")
+    if not isinstance(top_k, int) or isinstance(top_k, bool) or not (0 < top_k <= experts):
+        raise ValueError("top_k must be in [1, num_experts]")
+    _lib.require_device(router_logits, correction_bias)
+    logits = router_logits if router_logits.dtype == torch.float32 else router_logits.float()
+    bias = correction_bias if correction_bias.dtype == torch.float32 else correction_bias.float()
+    ids = torch.empty((tokens, top_k), dtype=torch.int32, device=router_logits.device)
+    weights = torch.empty((tokens, top_k), dtype=torch.float32, device=router_logits.device)
+    _lib.call("glm_moe_route_noaux_tc", _lib.ptr(logits.contiguous()), tokens, experts, _lib.ptr(bias.contiguous()),
+              top_k, _lib.ptr(ids), _lib.ptr(weights), _lib.stream_of(router_logits))
+    if _observe is not None:
+        _observe("router_selection", dict(indices=ids, weights=weights))
+    return ids, weights

@@ -63,6 +63,15 @@ const char* glm_moe_last_error(void);
 int glm_moe_decode_fp8_table(const uint8_t* bits, const float* scale, int64_t n, int64_t k,
                              int32_t block_n, int32_t block_k, uint16_t* out_bf16, void* stream);
 
+/* Replaces glm_tpu/layers/moe/router.py:20-55 route_glm_noaux_tc_logits: FP32
+ * sigmoid scores of logits [tokens, experts]; the top_k experts of scores + bias
+ * (bias may be NULL: zero), best first, ties to the lowest id; weights = the
+ * chosen unbiased scores over their FP32 sum.  ids int32 / weights f32
+ * [tokens, top_k].  experts <= 1024, top_k <= min(16, experts). */
+int glm_moe_route_noaux_tc(const float* router_logits, int64_t tokens, int32_t num_experts,
+                           const float* correction_bias, int32_t top_k, int32_t* route_indices,
+                           float* route_weights, void* stream);
+
 /* Replaces glm_tpu/layers/moe/routed_experts.py:139-164 group_prefill_routes:
  * sorted_flat_ids = argsort(flat ids, stable), inverse_permutation, group_sizes
  * = bincount (invalid ids count as expert 0), *valid = all ids in [0, E) and no

@@ -102,7 +102,7 @@ def bf16_from_bits(bits) -> np.ndarray:
 
 
 def sigmoid_f32(x) -> np.ndarray:
-    """FP32 logistic ``1 / (1 + exp(-x))`` (``jax.nn.sigmoid`` call sites, ``router.py:183``)."""
+    """FP32 logistic ``1 / (1 + exp(-x))`` (``jax.nn.sigmoid`` call sites, ``router.py:40``)."""
     x = np.asarray(x, np.float32)
     with np.errstate(over="ignore"):
         return (np.float32(1.0) / (np.float32(1.0) + np.exp(-x))).astype(np.float32)
@@ -497,7 +497,7 @@ def moe_layer(hidden, route_indices, route_weights, gate_bits, gate_scale, up_bi
 
 # ----------------------------------------------------------------------------- router
 def route_glm_noaux_tc_logits(router_logits, correction_bias, top_k: int = 8):
-    """GLM ``noaux_tc`` selection (``glm_tpu/layers/moe/router.py:163-198``).
+    """GLM ``noaux_tc`` selection (``glm_tpu/layers/moe/router.py:20-55``).
 
     FP32 sigmoid scores; the top-k of ``scores + bias`` with ties to the lowest
     id (``lax.top_k``); weights are the unbiased scores of the chosen experts

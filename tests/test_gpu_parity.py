@@ -501,3 +501,46 @@ def test_fp8_mode_production_shape_sampled_tokens(device, production_tables):
     err = np.abs(full[rows] - ref16)
     print(f"prefill_t2048 fp8 mode vs reference numerics: max-abs {err.max():.3e}, "
           f"mean-rel {err.mean() / np.abs(ref16).mean():.3e}")
+
+
+# ----------------------------------------------------------------------------- router (route_glm_noaux_tc_logits)
+def test_router_reference_known_answers(device):
+    """The reference's KATs (tests/layers/moe/test_router.py:51-65), exactly."""
+    from glm_moe.layers.moe.router import route_glm_noaux_tc_logits
+
+    logits = dev(np.float32([[3.0, 2.0, 1.0, 0.0]]), device)
+    bias = dev(np.float32([0.0, 0.0, 100.0, 99.0]), device)
+    ids, w = route_glm_noaux_tc_logits(logits, bias, top_k=2)
+    np.testing.assert_array_equal(ids.cpu().numpy(), [[2, 3]])
+    unbiased = O.sigmoid_f32(np.float32([1.0, 0.0]))
+    np.testing.assert_allclose(w.cpu().numpy()[0], unbiased / unbiased.sum(dtype=np.float32), rtol=1e-7, atol=0)
+    ids, w = route_glm_noaux_tc_logits(dev(np.zeros((1, 16), np.float32), device),
+                                       dev(np.zeros(16, np.float32), device), top_k=8)
+    np.testing.assert_array_equal(ids.cpu().numpy(), [list(range(8))])
+    np.testing.assert_array_equal(w.cpu().numpy(), np.full((1, 8), 0.125, np.float32))
+
+
+@pytest.mark.parametrize("tokens,experts,top_k,zipf,biased", [
+    (1, 256, 8, 0.0, False), (300, 256, 8, 0.0, True), (2048, 256, 8, 1.2, False), (64, 1024, 16, 0.0, True),
+    (5, 8, 2, 0.0, False),
+])
+def test_router_matches_oracle(device, tokens, experts, top_k, zipf, biased):
+    from glm_moe.layers.moe.router import route_glm_noaux_tc_logits
+
+    rng = np.random.default_rng(tokens + experts)
+    logits = rng.standard_normal((tokens, experts)).astype(np.float32)
+    if zipf:
+        r = np.arange(1, experts + 1, dtype=np.float64) ** -zipf
+        logits = (logits + np.log(r / r.sum()).astype(np.float32)).astype(np.float32)
+    bias = (rng.standard_normal(experts) * 0.1).astype(np.float32) if biased else np.zeros(experts, np.float32)
+    ids, w = route_glm_noaux_tc_logits(dev(logits, device), dev(bias, device), top_k=top_k)
+    ref_ids, ref_w = O.route_glm_noaux_tc_logits(logits, bias, top_k=top_k)
+    # selection is compared where the oracle's k-th and (k+1)-th biased scores are
+    # separated by more than the FP32 sigmoid rounding (a tie there is decided by
+    # the last bit of exp, which the reference's XLA does not pin either)
+    scores = O.sigmoid_f32(logits) + bias[None, :]
+    srt = -np.sort(-scores, axis=1)
+    clear = (srt[:, top_k - 1] - srt[:, top_k]) > 1e-6 if top_k < experts else np.ones(tokens, bool)
+    assert clear.mean() > 0.95
+    np.testing.assert_array_equal(ids.cpu().numpy()[clear], ref_ids[clear])
+    np.testing.assert_allclose(w.cpu().numpy()[clear], ref_w[clear], rtol=2e-6, atol=1e-7)

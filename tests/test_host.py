@@ -155,3 +155,23 @@ def test_algorithmic_bytes_of_the_decode_config():
     # 8 experts x 3 x 6144 x 2048 e4m3 bytes + scales + activations (302.1 MB)
     assert abs(b["total"] - 302.1e6) < 0.1e6
     assert S.algorithmic_flops(cfg)["total"] == 2 * 8 * 3 * 6144 * 2048
+
+
+def test_router_refuses_bad_geometry():
+    import torch
+
+    from glm_moe import _lib
+    from glm_moe.layers.moe.router import route_glm_noaux_tc_logits
+
+    lib = _lib.lib()
+    null = ctypes.c_void_p(0)
+    assert lib.glm_moe_route_noaux_tc(null, 4, 8, null, 9, null, null, null) == _lib.ERR_ARGUMENT
+    assert lib.glm_moe_route_noaux_tc(null, 4, 2048, null, 8, null, null, null) == _lib.ERR_ARGUMENT
+    with pytest.raises(ValueError, match="router_logits must have shape"):
+        route_glm_noaux_tc_logits(torch.zeros(8), torch.zeros(8))
+    with pytest.raises(ValueError, match="correction_bias"):
+        route_glm_noaux_tc_logits(torch.zeros(2, 8), torch.zeros(7))
+    with pytest.raises(ValueError, match="top_k must be in"):
+        route_glm_noaux_tc_logits(torch.zeros(2, 8), torch.zeros(8), top_k=9)
+    with pytest.raises(ValueError, match="GPU tensors only"):
+        route_glm_noaux_tc_logits(torch.zeros(2, 8), torch.zeros(8), top_k=2)
