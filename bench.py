@@ -164,6 +164,7 @@ DECODE_PATH_MAX_ROUTES = 64  # routes handled by the two decode GEMV kernels (li
 # raw counter summary are in the named profile.
 MEASURED_TRAFFIC = {
     ("decode_t1", "decode_gate_up_kernel"): {"bytes": 201.79e6, "source": "profiles/decode_t1_hbm_traffic.md"},
+    ("prefill_t2048", "prefill_gemm_kernel"): {"bytes": 6888.0e6, "source": "profiles/prefill_t2048_hbm_traffic.md"},
 }
 
 
@@ -186,7 +187,7 @@ def dominant_roofline(cfg, head):
         line = {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": achieved / HBM_PEAK_GBS}
     else:
-        kernel = "grouped_fp8_gemm_wide_kernel (gate/up, SwiGLU epilogue)"
+        kernel = "prefill_gemm_kernel"
         achieved = head["gate_up_tflops"]
         line = {"bound": "mfma", "achieved": achieved, "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                 "frac": achieved / BF16_PEAK_TFLOPS}
