@@ -88,19 +88,39 @@ __device__ __forceinline__ void load_lds_16(__amdgpu_buffer_rsrc_t rsrc, uint8_t
 #endif
 }
 
-template <int TABLES, int RG, int WAVES, int STAGES, int EPI>
+// Ring depths of one column-group variant, within 160 KB of LDS: SW weight
+// blocks (32 KB each: every wave's rows of the stripe) and SX activation stages
+// of XLOADS 1 KB loads per wave (NCG x 16 rows x 256 B, rounded up to whole
+// loads; the rows past NCG x 16 are loaded out of range and never read).
+// The weight stream is what HBM latency has to be hidden for: SW - 1 blocks
+// (64-96 KB per CU) stay in flight while one is consumed.
+template <int NCG, int WAVES>
+struct PrefillRings {
+  static constexpr int XLOADS = (NCG * 4 + WAVES - 1) / WAVES;
+  static constexpr int XSTAGE = XLOADS * WAVES * 1024;
+  static constexpr int SW = XSTAGE <= 8192 ? 4 : 3;
+  static constexpr int SX = XSTAGE <= 16384 ? 4 : 2;
+};
+constexpr int kStripeBlockBytes = 32768;  // e4m3 bytes of one work item's weight rows per K block
+constexpr int kPrefillLds = 160 * 1024;  // the whole LDS of a CU
+constexpr int kOutOfRange = 0x40000000;  // buffer offset beyond every descriptor's range: reads nothing, returns zeros
+
+// Loads a wave has issued after the later of block kb's activation and weight
+// loads, up to the barrier of iteration kb, when iteration i issues the
+// activations of block i + SX - 1 and then the weights of block i + SW - 1.
+constexpr int prefill_pending(int sw, int sx, int xloads, int wloads) {
+  return sx < sw ? wloads + (sx - 2) * (xloads + wloads) : (sw - 2) * (xloads + wloads);
+}
+
+template <int TABLES, int RG, int WAVES, int EPI>
 __global__ __launch_bounds__(64 * WAVES, 1) void prefill_gemm_kernel(const GroupedGemmArgs a) {
-  constexpr int BN = WAVES * RG * 16;                      // weight rows per table per work item
-  constexpr int XLOADS = kStageBytes / (WAVES * 1024);     // 1 KB activation loads per wave per K block
-  constexpr int WLOADS = TABLES * RG * 2;                  // 16-byte weight loads per lane per K block
-  // vector-memory loads a wave issues per K block (activations and weights, in any order)
-  constexpr int PER_BLOCK = XLOADS + WLOADS;
-  static_assert(XLOADS * WAVES * 1024 == kStageBytes, "activation stage split");
-  static_assert(STAGES % 2 == 0, "A operands alternate between two buffers");
-  // block kb is complete once at most the STAGES - 2 blocks issued after it are in flight
-  constexpr int X_PENDING = (STAGES - 2) * PER_BLOCK;
-  // [STAGES][kBM][256 B] activation ring, then per wave [TABLES * RG][16 rows][128 B] weight transposes
-  extern __shared__ __attribute__((aligned(16))) uint8_t xs[];
+  constexpr int BN = WAVES * RG * 16;  // weight rows per table per work item
+  constexpr int GROUPS = TABLES * RG;  // 16-row weight groups of one wave
+  constexpr int WLOADS = GROUPS * 2;   // 1 KB weight loads per wave per K block
+  constexpr int WAVE_BLOCK = GROUPS * 2048;  // e4m3 bytes of one wave's rows per K block
+  static_assert(WAVES * WAVE_BLOCK == kStripeBlockBytes, "32 KB of weight rows per work item per K block");
+  // [SW][WAVES][GROUPS][16 rows][128 B] weight ring, then [SX][NCG * 16 rows][256 B] activation ring
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
 
   if (a.valid != nullptr && a.valid[0] == 0) return;
   const int stripes = a.n / BN;
@@ -129,7 +149,7 @@ __global__ __launch_bounds__(64 * WAVES, 1) void prefill_gemm_kernel(const Group
   const int ncg = (live + 15) >> 4;
 
   const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wave = uniform(threadIdx.x >> 6);
   const int lrow = lane & 15;
   const int lgrp = lane >> 4;
   const int N = a.n;
@@ -137,204 +157,176 @@ __global__ __launch_bounds__(64 * WAVES, 1) void prefill_gemm_kernel(const Group
   const int KB = K / kScaleBlock;
   const int n0 = stripe * BN + wave * RG * 16;
 
-  // Loads are raw buffer loads: a loop-invariant per-lane VGPR offset, the K
-  // block as a scalar offset, the base and bounds in a scalar descriptor.
-  // ---- activation rows this lane loads: instruction i of a stage covers rows
-  // 4 * (wave * XLOADS + i) + lane / 16; the lane fetches the chunk whose slot is lane % 16
-  const __amdgpu_buffer_rsrc_t xrsrc = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<uint16_t*>(a.x), (short)0, (int)(a.x_rows * K * 2), kBufferFormat);
-  int xoff[XLOADS];
+  // Weight group g of this wave: table g / RG, rows n0 + (g % RG) * 16 .. +15.
+  // Load h of a group brings its rows 8h .. 8h+7 as whole 128-byte lines (lane
+  // l: row 8h + l/8), straight into LDS; the lane fetches chunk (l%8) ^ (l/8),
+  // so slot s of row r holds chunk s ^ (r % 8) and the MFMA-layout reads below
+  // (16 rows, one chunk each) hit distinct banks.  Block scales: one per lane
+  // (lane kb holds block kb; K <= 64 blocks), picked per block with v_readlane.
+  __amdgpu_buffer_rsrc_t wrsrc[GROUPS];
+  float sreg[GROUPS];
 #pragma unroll
-  for (int i = 0; i < XLOADS; ++i) {
-    const int row = 4 * (wave * XLOADS + i) + lgrp;
-    const int r = r0 + (row < live ? row : 0);  // padding rows repeat a live row; their columns are dropped
-    int64_t phys = a.x_row_ids ? a.x_row_ids[r] / a.x_row_div : r;
-    phys = phys < 0 ? 0 : (phys >= a.x_rows ? a.x_rows - 1 : phys);
-    xoff[i] = (int)(phys * K * 2) + ((lrow ^ (row & 15)) << 4);
-  }
-
-  // ---- weight rows of this wave: row n0 + rg * 16 + lane % 16, bytes (lane / 16) * 16 (+ 64);
-  // block scales of the rows' K blocks one per lane (lane kb holds block kb;
-  // K <= 64 blocks), picked per block with v_readlane
-  __amdgpu_buffer_rsrc_t wrsrc[TABLES][RG];
-  float sreg[TABLES][RG];
-  // 8 rows x 128 bytes per load (lane l: row 8h + l/8 of the 16, chunk l%8):
-  // every 128-byte line is fetched whole by one instruction, the pattern that
-  // streams HBM at full rate (half lines per instruction cap near 5.4 TB/s)
-  int woff[2];
-#pragma unroll
-  for (int h = 0; h < 2; ++h) woff[h] = (8 * h + (lane >> 3)) * K + (lane & 7) * 16;
-#pragma unroll
-  for (int t = 0; t < TABLES; ++t) {
+  for (int g = 0; g < GROUPS; ++g) {
+    const int t = g / RG, rg = g % RG;
     const uint8_t* wb = t == 0 ? a.w0 : a.w1;
     const float* sb = t == 0 ? a.s0 : a.s1;
-#pragma unroll
-    for (int rg = 0; rg < RG; ++rg) {
-      wrsrc[t][rg] = __builtin_amdgcn_make_buffer_rsrc(
-          const_cast<uint8_t*>(wb + ((size_t)e * N + n0 + rg * 16) * (size_t)K), (short)0, 16 * K, kBufferFormat);
-      const float* srow = sb + ((size_t)e * (N / kScaleBlock) + (n0 + rg * 16) / kScaleBlock) * KB;
-      sreg[t][rg] = lane < KB ? srow[lane] : 0.0f;
-    }
+    wrsrc[g] = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint8_t*>(wb + ((size_t)e * N + n0 + rg * 16) * (size_t)K), (short)0, 16 * K, kBufferFormat);
+    const float* srow = sb + ((size_t)e * (N / kScaleBlock) + (n0 + rg * 16) / kScaleBlock) * KB;
+    sreg[g] = lane < KB ? srow[lane] : 0.0f;
   }
+  const int woff = (lane >> 3) * K + (((lane & 7) ^ (lane >> 3)) << 4);
+  const __amdgpu_buffer_rsrc_t xrsrc = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t*>(a.x), (short)0, (int)(a.x_rows * K * 2), kBufferFormat);
 
-  f32x4 acc[TABLES][RG][kCG];
-#pragma unroll
-  for (int t = 0; t < TABLES; ++t)
-#pragma unroll
-    for (int rg = 0; rg < RG; ++rg)
-#pragma unroll
-      for (int cg = 0; cg < kCG; ++cg) acc[t][rg][cg] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-  // weights: two ring slots; block kb + 2 is issued while block kb + 1 is decoded
-  u32x4 wring[2][TABLES][RG][2];
-
-  // Issue block kb's activations into stage st, and block kw's weights into
-  // ring slot kw % 2 (both clamped to the last block: the pipeline always
-  // issues the same number of loads, so the wait counts stay exact).
-  auto issue = [&](int st, int kb, int kw) {
-    kb = kb < KB ? kb : KB - 1;
-    const int ws = kw & 1;
-    kw = kw < KB ? kw : KB - 1;
-    uint8_t* stage = xs + st * kStageBytes;
-#pragma unroll
-    for (int i = 0; i < XLOADS; ++i)
-      load_lds_16(xrsrc, stage + (wave * XLOADS + i) * 1024, xoff[i], kb * kRowBytes);
+  // One variant per column-group count (2, 4, 6 or 8 groups of 16 routes): the
+  // activation stage, the ring depths, the MFMA loop and the accumulators are
+  // compile-time, and each variant ends in its own epilogue.
+  auto run = [&](auto ncg_tag) {
+    constexpr int NCG = decltype(ncg_tag)::value;
+    f32x4 acc[TABLES][RG][NCG];
 #pragma unroll
     for (int t = 0; t < TABLES; ++t)
 #pragma unroll
-      for (int rg = 0; rg < RG; ++rg) {
+      for (int rg = 0; rg < RG; ++rg)
+#pragma unroll
+        for (int cg = 0; cg < NCG; ++cg) acc[t][rg][cg] = f32x4{0.f, 0.f, 0.f, 0.f};
+    using Rings = PrefillRings<NCG, WAVES>;
+    constexpr int SW = Rings::SW;
+    constexpr int SX = Rings::SX;
+    constexpr int XLOADS = Rings::XLOADS;  // 1 KB activation loads per wave per K block
+    constexpr int XSTAGE = Rings::XSTAGE;
+    static_assert(XSTAGE >= NCG * 16 * kRowBytes, "activation stage holds the tile's rows");
+    static_assert(SW * kStripeBlockBytes + SX * XSTAGE <= kPrefillLds, "LDS budget");
+    constexpr int PENDING = prefill_pending(SW, SX, XLOADS, WLOADS);
+    static_assert(PENDING >= 0 && PENDING < 64, "vmcnt range");
+    uint8_t* const wring = lds + wave * WAVE_BLOCK;     // slot s at + s * 32 KB
+    uint8_t* const xring = lds + SW * kStripeBlockBytes;  // stage s at + s * XSTAGE
+
+    // activation rows this lane loads: instruction i covers rows 4 * (wave *
+    // XLOADS + i) + lane / 16; the lane fetches the chunk whose slot is lane % 16
+    int xoff[XLOADS];
+#pragma unroll
+    for (int i = 0; i < XLOADS; ++i) {
+      const int row = 4 * (wave * XLOADS + i) + lgrp;
+      const int r = r0 + (row < live ? row : 0);  // padding rows repeat a live row; their columns are dropped
+      int64_t phys = a.x_row_ids ? a.x_row_ids[r] / a.x_row_div : r;
+      phys = phys < 0 ? 0 : (phys >= a.x_rows ? a.x_rows - 1 : phys);
+      xoff[i] = row < NCG * 16 ? (int)(phys * K * 2) + ((lrow ^ (row & 15)) << 4) : kOutOfRange;
+    }
+    // Blocks past the last one are issued out of range (no memory traffic, zeros
+    // into a slot nobody reads), so every iteration issues the same loads and
+    // the wait count stays exact.
+    auto issue_x = [&](int blk) {
+      uint8_t* st = xring + (blk % SX) * XSTAGE + wave * XLOADS * 1024;
+      const bool in = blk < KB;
+#pragma unroll
+      for (int i = 0; i < XLOADS; ++i)
+        load_lds_16(xrsrc, st + i * 1024, in ? xoff[i] : kOutOfRange, in ? blk * kRowBytes : 0);
+    };
+    auto issue_w = [&](int blk) {
+      uint8_t* st = wring + (blk % SW) * kStripeBlockBytes;
+      const bool in = blk < KB;
+#pragma unroll
+      for (int g = 0; g < GROUPS; ++g)
 #pragma unroll
         for (int h = 0; h < 2; ++h)
-          wring[ws][t][rg][h] = __builtin_bit_cast(
-              u32x4, __builtin_amdgcn_raw_buffer_load_b128(wrsrc[t][rg], woff[h], kw * kScaleBlock, kNonTemporal));
-      }
-  };
+          load_lds_16(wrsrc[g], st + (2 * g + h) * 1024, in ? woff + 8 * h * K : kOutOfRange,
+                      in ? blk * kScaleBlock : 0);
+    };
 
-  // Software pipeline inside each wave: while the MFMAs of block kb run (A
-  // operands decoded one block earlier), the VALU decodes block kb + 1 into the
-  // other A buffer, so the matrix cores and the vector ALU work at the same
-  // time.  The column-group count is a compile-time constant of each variant
-  // (2, 4, 6 or 8 groups of 16 routes), so the body has no branches and the
-  // scheduler may interleave ds_read, MFMA and decode instructions freely.
-  auto run = [&](auto ncg_tag) {
-    constexpr int NCG = decltype(ncg_tag)::value;
-    constexpr int NOPS = TABLES * RG * 4;  // bf16x8 A operands per block
-    bf16x8 A[2][TABLES][RG][4];
-    // Ring slot -> the wave's own LDS region (chunk c of row r in slot c ^ (r % 8))
-    // -> registers in MFMA A layout: lane l gets row l % 16, chunks l/16 and
-    // 4 + l/16 (K = g*16 .. +15 and 64 + g*16 .. +15 of the block).  Only this
-    // wave touches the region, and its LDS accesses run in order: no barrier.
-    uint8_t* wl = xs + STAGES * kStageBytes + wave * (TABLES * RG * 2048);
-    auto transpose = [&](int slot, u32x4 (&wt)[TABLES][RG][2]) {
+    // prologue: the issue schedule's iterations -P .. -1
+    constexpr int P = (SX > SW ? SX : SW) - 1;
 #pragma unroll
-      for (int t = 0; t < TABLES; ++t)
+    for (int i = -P; i < 0; ++i) {
+      if (i + SX - 1 >= 0) issue_x(i + SX - 1);
+      if (i + SW - 1 >= 0) issue_w(i + SW - 1);
+    }
+    for (int kb = 0; kb < KB; ++kb) {
+      // this wave's loads of block kb have landed; after the barrier everyone's
+      // have, and everyone is done with block kb - 1, whose slots are refilled now
+      wait_loads_then_barrier<PENDING>();
+      issue_x(kb + SX - 1);
+      issue_w(kb + SW - 1);
+
+      const uint8_t* wl = wring + (kb % SW) * kStripeBlockBytes;
+      const uint8_t* xl = xring + (kb % SX) * XSTAGE;
+      // this wave's rows in MFMA A layout: lane l gets row l % 16, chunks l/16
+      // and 4 + l/16 (K = g*16 .. +15 and 64 + g*16 .. +15 of the block)
+      u32x4 wbits[GROUPS][2];
 #pragma unroll
-        for (int rg = 0; rg < RG; ++rg)
+      for (int g = 0; g < GROUPS; ++g)
 #pragma unroll
-          for (int h = 0; h < 2; ++h) {
-            const int row = 8 * h + (lane >> 3);
-            *reinterpret_cast<u32x4*>(wl + (t * RG + rg) * 2048 + row * 128 + (((lane & 7) ^ (row & 7)) << 4)) =
-                wring[slot][t][rg][h];
-          }
+        for (int h = 0; h < 2; ++h)
+          wbits[g][h] =
+              *reinterpret_cast<const u32x4*>(wl + g * 2048 + lrow * 128 + (((lgrp + 4 * h) ^ (lrow & 7)) << 4));
+      float sc[GROUPS];
 #pragma unroll
-      for (int t = 0; t < TABLES; ++t)
+      for (int g = 0; g < GROUPS; ++g)
+        sc[g] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, sreg[g]), kb));
+      // Four 32-wide K steps, software-pipelined inside the wave: while the
+      // MFMAs of step q run on the matrix core, the VALU decodes step q + 1's
+      // A operands and the LDS delivers its B fragments.  Issue is in order, so
+      // the source order is the schedule: the next step's B reads first, then
+      // per weight group its MFMAs followed by its share of the next decode,
+      // fenced with scheduling barriers (the compiler would otherwise gather
+      // the decode into one block and run the VALU and the matrix core in turns).
+      auto decode_group = [&](int q, int g) -> bf16x8 {
+        const u32x4 w = wbits[g][q >> 1];
+        return (q & 1) ? decode_fp8x8(w.z, w.w, sc[g]) : decode_fp8x8(w.x, w.y, sc[g]);
+      };
+      auto read_b = [&](int q, bf16x8 (&B)[NCG]) {
 #pragma unroll
-        for (int rg = 0; rg < RG; ++rg)
+        for (int cg = 0; cg < NCG; ++cg) {
+          // B fragment of route row i for step q: logical chunk 2g + (q & 1) + 8 (q >> 1)
+          const int i = cg * 16 + lrow;
+          B[cg] = as_bf16x8(*reinterpret_cast<const u32x4*>(
+              xl + i * kRowBytes + (((2 * lgrp + (q & 1) + 8 * (q >> 1)) ^ (i & 15)) << 4)));
+        }
+      };
+      bf16x8 A[2][GROUPS];
+      bf16x8 B[2][NCG];
+      read_b(0, B[0]);
 #pragma unroll
-          for (int h = 0; h < 2; ++h)
-            wt[t][rg][h] = *reinterpret_cast<const u32x4*>(wl + (t * RG + rg) * 2048 + lrow * 128 +
-                                                            (((lgrp + 4 * h) ^ (lrow & 7)) << 4));
-    };
-    auto decode_op = [&](int o, const u32x4 (&wt)[TABLES][RG][2], float (&sc)[TABLES][RG],
-                         bf16x8 (&dst)[TABLES][RG][4]) {
-      const int t = o / (RG * 4), rg = (o / 4) % RG, q = o % 4;
-      const u32x4 w = wt[t][rg][q >> 1];
-      dst[t][rg][q] = (q & 1) ? decode_fp8x8(w.z, w.w, sc[t][rg]) : decode_fp8x8(w.x, w.y, sc[t][rg]);
-    };
-    auto scales_of = [&](int kb, float (&sc)[TABLES][RG]) {
-      kb = kb < KB ? kb : KB - 1;
+      for (int g = 0; g < GROUPS; ++g) A[0][g] = decode_group(0, g);
 #pragma unroll
-      for (int t = 0; t < TABLES; ++t)
-#pragma unroll
-        for (int rg = 0; rg < RG; ++rg)
-          sc[t][rg] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, sreg[t][rg]), kb));
-    };
-    // MFMAs of the block staged in `st` with operands A[cur]; decode of ring
-    // slot `next_slot` (block kb_next) into A[cur ^ 1], spread over the column groups
-    auto step = [&](int st, int cur, int next_slot, int kb_next) {
-      const uint8_t* stage = xs + st * kStageBytes;
-      float sc[TABLES][RG];
-      scales_of(kb_next, sc);
-      u32x4 wt[TABLES][RG][2];
-      transpose(next_slot, wt);
-#pragma unroll
-      for (int cg = 0; cg < NCG; ++cg) {
-        // B fragment j of route row i: logical chunks 2g, 2g+1, 8+2g, 8+2g+1 (the A K order)
-        const int i = cg * 16 + lrow;
-        const uint8_t* rowp = stage + i * kRowBytes;
-        const int sw = i & 15;
-        const bf16x8 b0 = as_bf16x8(*reinterpret_cast<const u32x4*>(rowp + (((2 * lgrp) ^ sw) << 4)));
-        const bf16x8 b1 = as_bf16x8(*reinterpret_cast<const u32x4*>(rowp + (((2 * lgrp + 1) ^ sw) << 4)));
-        const bf16x8 b2 = as_bf16x8(*reinterpret_cast<const u32x4*>(rowp + (((8 + 2 * lgrp) ^ sw) << 4)));
-        const bf16x8 b3 = as_bf16x8(*reinterpret_cast<const u32x4*>(rowp + (((9 + 2 * lgrp) ^ sw) << 4)));
-#pragma unroll
-        for (int t = 0; t < TABLES; ++t)
-#pragma unroll
-          for (int rg = 0; rg < RG; ++rg) {
-            f32x4 c = acc[t][rg][cg];
-            c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[cur][t][rg][0], b0, c, 0, 0, 0);
-            c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[cur][t][rg][1], b1, c, 0, 0, 0);
-            c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[cur][t][rg][2], b2, c, 0, 0, 0);
-            c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[cur][t][rg][3], b3, c, 0, 0, 0);
-            acc[t][rg][cg] = c;
-          }
-#pragma unroll
-        for (int o = cg * NOPS / NCG; o < (cg + 1) * NOPS / NCG; ++o) decode_op(o, wt, sc, A[cur ^ 1]);
-        // one column group at a time: the next group's B reads are not hoisted
-        // above this one (bounds the registers they hold)
+      for (int q = 0; q < 4; ++q) {
+        const int cur = q & 1;
+        if (q < 3) read_b(q + 1, B[cur ^ 1]);
         __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int g = 0; g < GROUPS; ++g) {
+#pragma unroll
+          for (int cg = 0; cg < NCG; ++cg)
+            acc[g / RG][g % RG][cg] =
+                __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[cur][g], B[cur][cg], acc[g / RG][g % RG][cg], 0, 0, 0);
+          __builtin_amdgcn_sched_barrier(0);
+          if (q < 3) A[cur ^ 1][g] = decode_group(q + 1, g);
+          __builtin_amdgcn_sched_barrier(0);
+        }
       }
-    };
-
-    // prologue: activations of blocks 0 .. STAGES-2 and weights of blocks 0
-    // and 1 in flight (STAGES - 1 >= 2 issues), block 0 decoded
-#pragma unroll
-    for (int st = 0; st < STAGES - 1; ++st) issue(st, st, st < 2 ? st : 1);
-    {
-      float sc[TABLES][RG];
-      scales_of(0, sc);
-      u32x4 wt[TABLES][RG][2];
-      transpose(0, wt);
-#pragma unroll
-      for (int o = 0; o < NOPS; ++o) decode_op(o, wt, sc, A[0]);
     }
-    // K loop unrolled by STAGES (KB % STAGES == 0) so that ring slots and A buffers are static
-    for (int kb0 = 0; kb0 < KB; kb0 += STAGES) {
+    wait_all_loads();  // no load may still target LDS when the workgroup ends
+
+    // Epilogue: lane holds rows n .. n+3 of route column cg*16 + lrow.
 #pragma unroll
-      for (int j = 0; j < STAGES; ++j) {
-        const int kb = kb0 + j;
-        // this wave's share of block kb has landed; after the barrier everyone's
-        // has, and everyone is done with block kb - 1, whose slot is refilled now
-        wait_loads_then_barrier<X_PENDING>();
-        issue((j + STAGES - 1) % STAGES, kb + STAGES - 1, kb + 2);
-        step(j, j & 1, (j + 1) & 1, kb + 1);
-      }
+    for (int cg = 0; cg < NCG; ++cg) {
+      const int col = cg * 16 + lrow;
+      if (col >= live) continue;
+#pragma unroll
+      for (int rg = 0; rg < RG; ++rg)
+        store_fragment<TABLES, EPI>(a, r0 + col, n0 + rg * 16 + lgrp * 4, acc[0][rg][cg], acc[TABLES - 1][rg][cg]);
     }
   };
-  if (ncg <= 2) run(std::integral_constant<int, 2>{});
-  else if (ncg <= 4) run(std::integral_constant<int, 4>{});
-  else if (ncg <= 6) run(std::integral_constant<int, 6>{});
-  else run(std::integral_constant<int, 8>{});
-  wait_all_loads();  // no load may still target LDS when the workgroup ends
-
-  // Epilogue: lane holds rows n .. n+3 of route column cg*16 + lrow.
-#pragma unroll
-  for (int cg = 0; cg < kCG; ++cg) {
-    const int col = cg * 16 + lrow;
-    if (cg >= ncg || col >= live) continue;
-#pragma unroll
-    for (int rg = 0; rg < RG; ++rg)
-      store_fragment<TABLES, EPI>(a, r0 + col, n0 + rg * 16 + lgrp * 4, acc[0][rg][cg], acc[TABLES - 1][rg][cg]);
+  switch (ncg) {
+    case 1: run(std::integral_constant<int, 1>{}); break;
+    case 2: run(std::integral_constant<int, 2>{}); break;
+    case 3: run(std::integral_constant<int, 3>{}); break;
+    case 4: run(std::integral_constant<int, 4>{}); break;
+    case 5: run(std::integral_constant<int, 5>{}); break;
+    case 6: run(std::integral_constant<int, 6>{}); break;
+    case 7: run(std::integral_constant<int, 7>{}); break;
+    default: run(std::integral_constant<int, 8>{}); break;
   }
 }
 
@@ -576,24 +568,22 @@ hipError_t launch_prefill_fp8(const GroupedGemmArgs& a, hipStream_t stream) {
                        dim3(64 * WAVES), lds, stream, a);
 }
 
-template <int TABLES, int RG, int WAVES, int STAGES, int EPI>
+template <int TABLES, int RG, int WAVES, int EPI>
 hipError_t launch_prefill(const GroupedGemmArgs& a, hipStream_t stream) {
   constexpr int BN = WAVES * RG * 16;
-  const size_t lds = (size_t)STAGES * kStageBytes + (size_t)WAVES * TABLES * RG * 2048;
   static bool attr_set = false;  // one attribute call per instantiation (idempotent)
   if (!attr_set) {
-    const hipError_t err = hipFuncSetAttribute(
-        reinterpret_cast<const void*>(prefill_gemm_kernel<TABLES, RG, WAVES, STAGES, EPI>),
-        hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    const hipError_t err =
+        hipFuncSetAttribute(reinterpret_cast<const void*>(prefill_gemm_kernel<TABLES, RG, WAVES, EPI>),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, kPrefillLds);
     if (err != hipSuccess) return err;
     attr_set = true;
   }
   const int64_t items = (int64_t)(a.n / BN) * a.max_tiles;
   const int64_t grid = (items + kXcds - 1) / kXcds * kXcds;
-  return launch_kernel(prefill_gemm_kernel<TABLES, RG, WAVES, STAGES, EPI>, dim3((unsigned)grid), dim3(64 * WAVES),
-                       lds, stream, a);
+  return launch_kernel(prefill_gemm_kernel<TABLES, RG, WAVES, EPI>, dim3((unsigned)grid), dim3(64 * WAVES),
+                       (size_t)kPrefillLds, stream, a);
 }
-
 }  // namespace
 
 // Weight rows per table per work item of the prefill kernel.
@@ -620,8 +610,8 @@ hipError_t launch_grouped_gemm_prefill(const GroupedGemmArgs& a, int tables, int
       return launch_prefill_fp8<1, 2, 8, kPrefillStages, kEpiWeighted>(a, stream);
     return hipErrorInvalidValue;
   }
-  if (tables == 2 && epilogue == kEpiSwiglu) return launch_prefill<2, 1, 8, kPrefillStages, kEpiSwiglu>(a, stream);
-  if (tables == 1 && epilogue == kEpiWeighted) return launch_prefill<1, 2, 8, kPrefillStages, kEpiWeighted>(a, stream);
+  if (tables == 2 && epilogue == kEpiSwiglu) return launch_prefill<2, 1, 8, kEpiSwiglu>(a, stream);
+  if (tables == 1 && epilogue == kEpiWeighted) return launch_prefill<1, 2, 8, kEpiWeighted>(a, stream);
   return hipErrorInvalidValue;
 }
 
