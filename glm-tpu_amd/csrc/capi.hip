@@ -170,8 +170,8 @@ int routed_experts_impl(const uint16_t* hidden, int64_t tokens, int64_t hidden_s
   const bool fp8 = (flags & GLM_MOE_FP8_ACTIVATIONS) != 0;
   GLM_REQUIRE(!fp8 || (!uses_decode_path(n, hidden_size, intermediate) && shape == kShapeWide &&
                        prefill_fits(intermediate, hidden_size, 2) && prefill_fits(hidden_size, intermediate, 1)),
-              "FP8 activations need a prefill shape: more than 8 routes per expert on average, H and I multiples "
-              "of 512 (at most 8192), I a multiple of 128 rows per stripe");
+              "FP8 activations need a prefill shape: more than 8 routes per expert on average, H a multiple of "
+              "256 and I of 128, both at most 8192");
   const int bn13 = gemm_shape_bn(shape, 2);
   const int bn2 = gemm_shape_bn(shape, 1);
   GLM_REQUIRE(intermediate % bn13 == 0, "intermediate size must be a multiple of %d", bn13);

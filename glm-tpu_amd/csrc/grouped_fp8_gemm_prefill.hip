@@ -7,20 +7,24 @@
 // glm_tpu/kernels/fp8_grouped_matmul/panel_kernel.py:83-101).
 //
 // Work item = (expert, tile of <= 128 sorted routes, stripe of BN weight rows).
-//   * Each of the WAVES waves owns RG x 16 rows of every table of the stripe.
-//     It loads them straight into registers in MFMA A layout (lane l: row l%16,
-//     16 bytes at K offset (l/16)*16 and 64 + (l/16)*16 of the block), STAGES
-//     K blocks ahead, and decodes each byte once.  A weight byte is therefore
-//     read from HBM and decoded exactly once per work item.
+//   * Each of the 8 waves owns RG x 16 rows of every table of the stripe
+//     (32 KB of e4m3 bytes per K block for the work item).  The rows go HBM ->
+//     LDS with direct-to-LDS buffer loads (no registers), 8 rows x 128 bytes
+//     per instruction (whole lines), into a ring of SW blocks private to the
+//     wave, so SW - 1 blocks (64-96 KB per CU) stay in flight; chunk c of row r
+//     sits in slot c ^ (r % 8) so the MFMA-layout reads hit distinct banks.
+//     Every byte is decoded once per work item, one 32-wide K step ahead of
+//     the MFMAs that use it.
 //   * The tile's activation rows (gathered token rows for gate/up, sorted
-//     activation rows for down) go HBM/L2 -> LDS with direct-to-LDS loads
-//     (global_load_lds_dwordx4, no registers) into a ring of STAGES K blocks.
-//     Each 1 KB load covers 4 rows x 256 bytes; chunk c of row r is stored in
-//     slot c ^ (r % 16), so that the 16 lanes reading one MFMA B fragment hit
-//     distinct banks.  All waves share the staged rows as the B operand.
-//   * One workgroup barrier per K block; when it is passed, the block's rows
-//     are in LDS and every wave has finished with the block STAGES - 1 back,
-//     whose slot is refilled next.
+//     activation rows for down) go HBM/L2 -> LDS the same way into a ring of
+//     SX stages shared by all waves as the B operand; each 1 KB load covers 4
+//     rows x 256 bytes, chunk c of row r in slot c ^ (r % 16).
+//   * One workgroup barrier per K block: after it the block's rows are in LDS
+//     and every wave is done with the previous block, whose slots are refilled.
+//     Ring slots are runtime indices, so any K / 128 <= 64 works; blocks past
+//     the last are loaded out of range (no traffic) to keep wait counts exact.
+//   * One code variant per count of 16-route column groups (1..8), each with
+//     its own accumulators, ring depths and epilogue.
 // Work items are ordered expert-major, then in blocks of route tiles x
 // stripes (item_of_expert), and laid out XCD-aware: workgroup b runs on XCD
 // b % 8, and XCD x walks the contiguous range [x * per, (x + 1) * per) of work
@@ -45,7 +49,6 @@ constexpr int kBM = 128;           // routes per tile
 constexpr int kCG = kBM / 16;      // 16-route column groups
 constexpr int kXcds = 8;           // MI355X: 8 XCDs, workgroups dealt round-robin
 constexpr int kRowBytes = kScaleBlock * 2;   // one staged activation row of a K block (bf16)
-constexpr int kStageBytes = kBM * kRowBytes; // 32 KB
 
 // This wave's loads but the newest N have completed (direct-to-LDS loads
 // included: their data is in LDS); its LDS reads have completed; then the
@@ -81,10 +84,12 @@ __device__ __forceinline__ void wait_all_loads() { asm volatile("s_waitcnt vmcnt
 // 16 bytes a lane from rsrc + voffset + soffset straight into LDS at
 // lds + 16 * lane (buffer_load_dwordx4 ... lds).  The builtin only exists for
 // the device target; the host pass of the kernel template must not see it.
+// AUX is the cache policy (kNonTemporal for bytes that are read only once).
+template <int AUX = 0>
 __device__ __forceinline__ void load_lds_16(__amdgpu_buffer_rsrc_t rsrc, uint8_t* lds, int voffset, int soffset) {
 #if defined(__HIP_DEVICE_COMPILE__)
   __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (__attribute__((address_space(3))) void*)lds, 16, voffset, soffset,
-                                           0, 0);
+                                           0, AUX);
 #endif
 }
 
@@ -231,7 +236,7 @@ __global__ __launch_bounds__(64 * WAVES, 1) void prefill_gemm_kernel(const Group
       for (int g = 0; g < GROUPS; ++g)
 #pragma unroll
         for (int h = 0; h < 2; ++h)
-          load_lds_16(wrsrc[g], st + (2 * g + h) * 1024, in ? woff + 8 * h * K : kOutOfRange,
+          load_lds_16<kNonTemporal>(wrsrc[g], st + (2 * g + h) * 1024, in ? woff + 8 * h * K : kOutOfRange,
                       in ? blk * kScaleBlock : 0);
     };
 
@@ -347,18 +352,31 @@ __device__ __forceinline__ i32x8 join_i32x8(const u32x4& lo, const u32x4& hi) {
   return __builtin_shufflevector(l, h, 0, 1, 2, 3, 4, 5, 6, 7);
 }
 
-template <int TABLES, int RG, int WAVES, int STAGES, int EPI>
+// Ring depths of the FP8 kernel: SW weight blocks (32 KB) and SX activation
+// stages of XLOADS 1 KB loads per wave (NCG x 16 rows x 128 e4m3 bytes,
+// rounded up to whole loads), each with a 256-byte activation-scale slice per
+// wave (waves 0 and 1 hold the tile's 128 FP32 block scales).
+template <int NCG, int WAVES>
+struct Fp8Rings {
+  static constexpr int XLOADS = (NCG * 2 + WAVES - 1) / WAVES;
+  static constexpr int XSTAGE = XLOADS * WAVES * 1024;
+  static constexpr int SW = 3;
+  static constexpr int SX = XLOADS == 1 ? 4 : 3;
+};
+
+template <int TABLES, int RG, int WAVES, int EPI>
 __global__ __launch_bounds__(64 * WAVES, 1) void prefill_gemm_fp8_kernel(const GroupedGemmArgs a) {
   constexpr int BN = WAVES * RG * 16;
-  constexpr int ROWB = kScaleBlock;                          // e4m3 bytes of one activation row per K block
-  constexpr int STAGE = kBM * ROWB;                          // 16 KB
-  constexpr int XLOADS = STAGE / (WAVES * 1024);             // 1 KB activation loads per wave per K block
-  constexpr int WLOADS = TABLES * RG * 2;
-  constexpr int PER_BLOCK = XLOADS + 2 + WLOADS;             // + the two activation-scale loads
-  static_assert(XLOADS * WAVES * 1024 == STAGE, "activation stage split");
-  static_assert(STAGES % 2 == 0, "weight ring slots alternate");
-  constexpr int X_PENDING = (STAGES - 2) * PER_BLOCK;
-  extern __shared__ __attribute__((aligned(16))) uint8_t xs[];  // [STAGES][kBM][128 B], then weight transposes
+  constexpr int GROUPS = TABLES * RG;
+  constexpr int WLOADS = GROUPS * 2;
+  constexpr int WAVE_BLOCK = GROUPS * 2048;
+  static_assert(WAVES * WAVE_BLOCK == kStripeBlockBytes, "32 KB of weight rows per work item per K block");
+  static_assert(WAVES >= 2, "two waves load the activation scales");
+  constexpr int ROWB = kScaleBlock;  // e4m3 bytes of one activation row per K block
+  constexpr int SSTAGE = WAVES * 256;  // activation-scale slices of one stage
+  // [SW][WAVES][GROUPS][16 rows][128 B] weight ring, [SX][rows][128 B] activation
+  // ring, [SX][128] FP32 activation-scale ring
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
 
   if (a.valid != nullptr && a.valid[0] == 0) return;
   const int stripes = a.n / BN;
@@ -383,191 +401,177 @@ __global__ __launch_bounds__(64 * WAVES, 1) void prefill_gemm_fp8_kernel(const G
   const int ncg = (live + 15) >> 4;
 
   const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wave = uniform(threadIdx.x >> 6);
   const int lrow = lane & 15;
   const int lgrp = lane >> 4;
   const int N = a.n;
   const int K = a.k;
   const int KB = K / kScaleBlock;
   const int n0 = stripe * BN + wave * RG * 16;
-
   auto phys_row = [&](int row) -> int64_t {
     const int r = r0 + (row < live ? row : 0);  // padding rows repeat a live row; their columns are dropped
     int64_t phys = a.x_row_ids ? a.x_row_ids[r] / a.x_row_div : r;
     return phys < 0 ? 0 : (phys >= a.x_rows ? a.x_rows - 1 : phys);
   };
-  // activations: instruction i covers rows 8 * (wave * XLOADS + i) + lane / 8,
-  // 128 bytes each; chunk c of row r lands in slot c ^ (r % 8)
-  const __amdgpu_buffer_rsrc_t xrsrc = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<uint8_t*>(a.xq), (short)0, (int)(a.x_rows * K), kBufferFormat);
-  int xoff[XLOADS];
-#pragma unroll
-  for (int i = 0; i < XLOADS; ++i) {
-    const int row = 8 * (wave * XLOADS + i) + (lane >> 3);
-    xoff[i] = (int)(phys_row(row) * K) + (((lane & 7) ^ (row & 7)) << 4);
-  }
-  // activation block scales: this lane fetches those of tile rows lane and lane + 64
-  const __amdgpu_buffer_rsrc_t srsrc = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<float*>(a.xscale), (short)0, (int)(a.x_rows * KB * 4), kBufferFormat);
-  int soff[2];
-#pragma unroll
-  for (int h = 0; h < 2; ++h) soff[h] = (int)(phys_row(lane + 64 * h) * KB * 4);
 
-  __amdgpu_buffer_rsrc_t wrsrc[TABLES][RG];
-  float sreg[TABLES][RG];
-  int woff[2];
+  // weights: as in the bf16 kernel (direct-to-LDS, chunk c of row r in slot c ^ (r % 8))
+  __amdgpu_buffer_rsrc_t wrsrc[GROUPS];
+  float sreg[GROUPS];
 #pragma unroll
-  for (int h = 0; h < 2; ++h) woff[h] = (8 * h + (lane >> 3)) * K + (lane & 7) * 16;
-#pragma unroll
-  for (int t = 0; t < TABLES; ++t) {
+  for (int g = 0; g < GROUPS; ++g) {
+    const int t = g / RG, rg = g % RG;
     const uint8_t* wb = t == 0 ? a.w0 : a.w1;
     const float* sb = t == 0 ? a.s0 : a.s1;
-#pragma unroll
-    for (int rg = 0; rg < RG; ++rg) {
-      wrsrc[t][rg] = __builtin_amdgcn_make_buffer_rsrc(
-          const_cast<uint8_t*>(wb + ((size_t)e * N + n0 + rg * 16) * (size_t)K), (short)0, 16 * K, kBufferFormat);
-      const float* srow = sb + ((size_t)e * (N / kScaleBlock) + (n0 + rg * 16) / kScaleBlock) * KB;
-      sreg[t][rg] = lane < KB ? srow[lane] : 0.0f;
-    }
+    wrsrc[g] = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint8_t*>(wb + ((size_t)e * N + n0 + rg * 16) * (size_t)K), (short)0, 16 * K, kBufferFormat);
+    const float* srow = sb + ((size_t)e * (N / kScaleBlock) + (n0 + rg * 16) / kScaleBlock) * KB;
+    sreg[g] = lane < KB ? srow[lane] : 0.0f;
   }
-
-  f32x4 acc[TABLES][RG][kCG];
-#pragma unroll
-  for (int t = 0; t < TABLES; ++t)
-#pragma unroll
-    for (int rg = 0; rg < RG; ++rg)
-#pragma unroll
-      for (int cg = 0; cg < kCG; ++cg) acc[t][rg][cg] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-  u32x4 wring[2][TABLES][RG][2];
-  float sxr[STAGES][2];
-
-  auto issue = [&](int st, int kb, int kw) {
-    kb = kb < KB ? kb : KB - 1;
-    const int ws = kw & 1;
-    kw = kw < KB ? kw : KB - 1;
-    uint8_t* stage = xs + st * STAGE;
-#pragma unroll
-    for (int i = 0; i < XLOADS; ++i) load_lds_16(xrsrc, stage + (wave * XLOADS + i) * 1024, xoff[i], kb * ROWB);
-#pragma unroll
-    for (int h = 0; h < 2; ++h)
-      sxr[st][h] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(srsrc, soff[h], kb * 4, 0));
-#pragma unroll
-    for (int t = 0; t < TABLES; ++t)
-#pragma unroll
-      for (int rg = 0; rg < RG; ++rg)
-#pragma unroll
-        for (int h = 0; h < 2; ++h)
-          wring[ws][t][rg][h] = __builtin_bit_cast(
-              u32x4, __builtin_amdgcn_raw_buffer_load_b128(wrsrc[t][rg], woff[h], kw * kScaleBlock, kNonTemporal));
-  };
-
-  // weight ring slot -> this wave's LDS region -> MFMA A layout: lane l gets
-  // row l % 16, chunks 2 * (l / 16) and 2 * (l / 16) + 1 (32 e4m3 values)
-  uint8_t* wl = xs + STAGES * STAGE + wave * (TABLES * RG * 2048);
-  auto transpose = [&](int slot, u32x4 (&wt)[TABLES][RG][2]) {
-#pragma unroll
-    for (int t = 0; t < TABLES; ++t)
-#pragma unroll
-      for (int rg = 0; rg < RG; ++rg)
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-          const int row = 8 * h + (lane >> 3);
-          *reinterpret_cast<u32x4*>(wl + (t * RG + rg) * 2048 + row * 128 + (((lane & 7) ^ (row & 7)) << 4)) =
-              wring[slot][t][rg][h];
-        }
-#pragma unroll
-    for (int t = 0; t < TABLES; ++t)
-#pragma unroll
-      for (int rg = 0; rg < RG; ++rg)
-#pragma unroll
-        for (int h = 0; h < 2; ++h)
-          wt[t][rg][h] = *reinterpret_cast<const u32x4*>(wl + (t * RG + rg) * 2048 + lrow * 128 +
-                                                          (((2 * lgrp + h) ^ (lrow & 7)) << 4));
-  };
+  const int woff = (lane >> 3) * K + (((lane & 7) ^ (lane >> 3)) << 4);
+  const __amdgpu_buffer_rsrc_t xrsrc = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint8_t*>(a.xq), (short)0, (int)(a.x_rows * K), kBufferFormat);
+  // activation block scales: waves 0 and 1 load tile rows 64 w + lane of each
+  // block (4 bytes a lane); the other waves issue the same load out of range
+  // into their own slices, so that every wave's wait count is the same
+  const __amdgpu_buffer_rsrc_t srsrc = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<float*>(a.xscale), (short)0, (int)(a.x_rows * KB * 4), kBufferFormat);
+  const int soff = wave < 2 ? (int)(phys_row(64 * wave + lane) * KB * 4) : kOutOfRange;
 
   auto run = [&](auto ncg_tag) {
     constexpr int NCG = decltype(ncg_tag)::value;
-    auto step = [&](int st, const u32x4 (&wt)[TABLES][RG][2], int kb) {
-      const uint8_t* stage = xs + st * STAGE;
-      float sw[TABLES][RG];
+    using Rings = Fp8Rings<NCG, WAVES>;
+    constexpr int SW = Rings::SW;
+    constexpr int SX = Rings::SX;
+    constexpr int XLOADS = Rings::XLOADS;
+    constexpr int XSTAGE = Rings::XSTAGE;
+    static_assert(XSTAGE >= NCG * 16 * ROWB, "activation stage holds the tile's rows");
+    static_assert(SW * kStripeBlockBytes + SX * (XSTAGE + SSTAGE) <= kPrefillLds, "LDS budget");
+    constexpr int PENDING = prefill_pending(SW, SX, XLOADS + 1, WLOADS);
+    static_assert(PENDING >= 0 && PENDING < 64, "vmcnt range");
+    f32x4 acc[TABLES][RG][NCG];
 #pragma unroll
-      for (int t = 0; t < TABLES; ++t)
+    for (int t = 0; t < TABLES; ++t)
 #pragma unroll
-        for (int rg = 0; rg < RG; ++rg)
-          sw[t][rg] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, sreg[t][rg]), kb));
+      for (int rg = 0; rg < RG; ++rg)
+#pragma unroll
+        for (int cg = 0; cg < NCG; ++cg) acc[t][rg][cg] = f32x4{0.f, 0.f, 0.f, 0.f};
+    uint8_t* const wring = lds + wave * WAVE_BLOCK;
+    uint8_t* const xring = lds + SW * kStripeBlockBytes;
+    uint8_t* const sring = xring + SX * XSTAGE;
+
+    // activation rows: instruction i covers rows 8 * (wave * XLOADS + i) + lane / 8,
+    // 128 bytes each; chunk c of row r lands in slot c ^ (r % 8)
+    int xoff[XLOADS];
+#pragma unroll
+    for (int i = 0; i < XLOADS; ++i) {
+      const int row = 8 * (wave * XLOADS + i) + (lane >> 3);
+      xoff[i] = row < NCG * 16 ? (int)(phys_row(row) * K) + (((lane & 7) ^ (row & 7)) << 4) : kOutOfRange;
+    }
+    auto issue_x = [&](int blk) {
+      uint8_t* st = xring + (blk % SX) * XSTAGE + wave * XLOADS * 1024;
+      const bool in = blk < KB;
+#pragma unroll
+      for (int i = 0; i < XLOADS; ++i)
+        load_lds_16(xrsrc, st + i * 1024, in ? xoff[i] : kOutOfRange, in ? blk * ROWB : 0);
+#if defined(__HIP_DEVICE_COMPILE__)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          srsrc, (__attribute__((address_space(3))) void*)(sring + (blk % SX) * SSTAGE + wave * 256), 4,
+          in ? soff : kOutOfRange, in ? blk * 4 : 0, 0, 0);
+#endif
+    };
+    auto issue_w = [&](int blk) {
+      uint8_t* st = wring + (blk % SW) * kStripeBlockBytes;
+      const bool in = blk < KB;
+#pragma unroll
+      for (int g = 0; g < GROUPS; ++g)
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+          load_lds_16<kNonTemporal>(wrsrc[g], st + (2 * g + h) * 1024, in ? woff + 8 * h * K : kOutOfRange,
+                      in ? blk * kScaleBlock : 0);
+    };
+
+    constexpr int P = (SX > SW ? SX : SW) - 1;
+#pragma unroll
+    for (int i = -P; i < 0; ++i) {
+      if (i + SX - 1 >= 0) issue_x(i + SX - 1);
+      if (i + SW - 1 >= 0) issue_w(i + SW - 1);
+    }
+    for (int kb = 0; kb < KB; ++kb) {
+      wait_loads_then_barrier<PENDING>();
+      issue_x(kb + SX - 1);
+      issue_w(kb + SW - 1);
+
+      const uint8_t* wl = wring + (kb % SW) * kStripeBlockBytes;
+      const uint8_t* xl = xring + (kb % SX) * XSTAGE;
+      const float* sl = reinterpret_cast<const float*>(sring + (kb % SX) * SSTAGE);
+      // A: lane l gets row l % 16, chunks 2 (l/16) and 2 (l/16) + 1 (32 e4m3 values)
+      i32x8 wv[GROUPS];
+#pragma unroll
+      for (int g = 0; g < GROUPS; ++g)
+        wv[g] = join_i32x8(
+            *reinterpret_cast<const u32x4*>(wl + g * 2048 + lrow * 128 + (((2 * lgrp) ^ (lrow & 7)) << 4)),
+            *reinterpret_cast<const u32x4*>(wl + g * 2048 + lrow * 128 + (((2 * lgrp + 1) ^ (lrow & 7)) << 4)));
+      float sw[GROUPS];
+#pragma unroll
+      for (int g = 0; g < GROUPS; ++g)
+        sw[g] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, sreg[g]), kb));
 #pragma unroll
       for (int cg = 0; cg < NCG; ++cg) {
         const int i = cg * 16 + lrow;
-        const uint8_t* rowp = stage + i * ROWB;
-        const u32x4 b0 = *reinterpret_cast<const u32x4*>(rowp + (((2 * lgrp) ^ (i & 7)) << 4));
-        const u32x4 b1 = *reinterpret_cast<const u32x4*>(rowp + (((2 * lgrp + 1) ^ (i & 7)) << 4));
-        const i32x8 bv = join_i32x8(b0, b1);
-        // scale of route column i: held by lane i % 64 of half i / 64
-        const float sx = __shfl(sxr[st][cg >> 2], (cg & 3) * 16 + lrow, 64);
+        const uint8_t* rowp = xl + i * ROWB;
+        const i32x8 bv = join_i32x8(*reinterpret_cast<const u32x4*>(rowp + (((2 * lgrp) ^ (i & 7)) << 4)),
+                                    *reinterpret_cast<const u32x4*>(rowp + (((2 * lgrp + 1) ^ (i & 7)) << 4)));
+        const float sx = sl[i];
 #pragma unroll
-        for (int t = 0; t < TABLES; ++t)
+        for (int g = 0; g < GROUPS; ++g) {
+          const f32x4 p = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(wv[g], bv, f32x4{0.f, 0.f, 0.f, 0.f}, 0,
+                                                                           0, 0, 127, 0, 127);
+          const float f = sw[g] * sx;
+          f32x4 c = acc[g / RG][g % RG][cg];
 #pragma unroll
-          for (int rg = 0; rg < RG; ++rg) {
-            const f32x4 p = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
-                join_i32x8(wt[t][rg][0], wt[t][rg][1]), bv, f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0, 127, 0, 127);
-            const float f = sw[t][rg] * sx;
-            f32x4 c = acc[t][rg][cg];
-#pragma unroll
-            for (int j = 0; j < 4; ++j) c[j] = __builtin_fmaf(p[j], f, c[j]);
-            acc[t][rg][cg] = c;
-          }
-        __builtin_amdgcn_sched_barrier(0);
-      }
-    };
-#pragma unroll
-    for (int st = 0; st < STAGES - 1; ++st) issue(st, st, st < 2 ? st : 1);
-    for (int kb0 = 0; kb0 < KB; kb0 += STAGES) {
-#pragma unroll
-      for (int j = 0; j < STAGES; ++j) {
-        const int kb = kb0 + j;
-        wait_loads_then_barrier<X_PENDING>();
-        u32x4 wt[TABLES][RG][2];
-        transpose(j & 1, wt);  // weights of block kb leave their ring slot ...
-        issue((j + STAGES - 1) % STAGES, kb + STAGES - 1, kb + 2);  // ... which block kb + 2 refills
-        step(j, wt, kb);
+          for (int j = 0; j < 4; ++j) c[j] = __builtin_fmaf(p[j], f, c[j]);
+          acc[g / RG][g % RG][cg] = c;
+        }
       }
     }
+    wait_all_loads();
+#pragma unroll
+    for (int cg = 0; cg < NCG; ++cg) {
+      const int col = cg * 16 + lrow;
+      if (col >= live) continue;
+#pragma unroll
+      for (int rg = 0; rg < RG; ++rg)
+        store_fragment<TABLES, EPI>(a, r0 + col, n0 + rg * 16 + lgrp * 4, acc[0][rg][cg], acc[TABLES - 1][rg][cg]);
+    }
   };
-  if (ncg <= 2) run(std::integral_constant<int, 2>{});
-  else if (ncg <= 4) run(std::integral_constant<int, 4>{});
-  else if (ncg <= 6) run(std::integral_constant<int, 6>{});
-  else run(std::integral_constant<int, 8>{});
-  wait_all_loads();
-
-#pragma unroll
-  for (int cg = 0; cg < kCG; ++cg) {
-    const int col = cg * 16 + lrow;
-    if (cg >= ncg || col >= live) continue;
-#pragma unroll
-    for (int rg = 0; rg < RG; ++rg)
-      store_fragment<TABLES, EPI>(a, r0 + col, n0 + rg * 16 + lgrp * 4, acc[0][rg][cg], acc[TABLES - 1][rg][cg]);
+  switch (ncg) {
+    case 1: run(std::integral_constant<int, 1>{}); break;
+    case 2: run(std::integral_constant<int, 2>{}); break;
+    case 3: run(std::integral_constant<int, 3>{}); break;
+    case 4: run(std::integral_constant<int, 4>{}); break;
+    case 5: run(std::integral_constant<int, 5>{}); break;
+    case 6: run(std::integral_constant<int, 6>{}); break;
+    case 7: run(std::integral_constant<int, 7>{}); break;
+    default: run(std::integral_constant<int, 8>{}); break;
   }
 }
 
-template <int TABLES, int RG, int WAVES, int STAGES, int EPI>
+template <int TABLES, int RG, int WAVES, int EPI>
 hipError_t launch_prefill_fp8(const GroupedGemmArgs& a, hipStream_t stream) {
   constexpr int BN = WAVES * RG * 16;
-  const size_t lds = (size_t)STAGES * kBM * kScaleBlock + (size_t)WAVES * TABLES * RG * 2048;
   static bool attr_set = false;
   if (!attr_set) {
-    const hipError_t err = hipFuncSetAttribute(
-        reinterpret_cast<const void*>(prefill_gemm_fp8_kernel<TABLES, RG, WAVES, STAGES, EPI>),
-        hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    const hipError_t err =
+        hipFuncSetAttribute(reinterpret_cast<const void*>(prefill_gemm_fp8_kernel<TABLES, RG, WAVES, EPI>),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, kPrefillLds);
     if (err != hipSuccess) return err;
     attr_set = true;
   }
   const int64_t items = (int64_t)(a.n / BN) * a.max_tiles;
   const int64_t grid = (items + kXcds - 1) / kXcds * kXcds;
-  return launch_kernel(prefill_gemm_fp8_kernel<TABLES, RG, WAVES, STAGES, EPI>, dim3((unsigned)grid),
-                       dim3(64 * WAVES), lds, stream, a);
+  return launch_kernel(prefill_gemm_fp8_kernel<TABLES, RG, WAVES, EPI>, dim3((unsigned)grid), dim3(64 * WAVES),
+                       (size_t)kPrefillLds, stream, a);
 }
-
 template <int TABLES, int RG, int WAVES, int EPI>
 hipError_t launch_prefill(const GroupedGemmArgs& a, hipStream_t stream) {
   constexpr int BN = WAVES * RG * 16;
@@ -589,15 +593,10 @@ hipError_t launch_prefill(const GroupedGemmArgs& a, hipStream_t stream) {
 // Weight rows per table per work item of the prefill kernel.
 int prefill_bn(int tables) { return tables == 2 ? 8 * 16 : 8 * 32; }
 
-constexpr int kPrefillStages = 4;
-
-// The prefill kernel holds one block scale per lane (K <= 64 blocks of 128)
-// and unrolls its K loop by its stage count (K blocks a multiple of it).
+// The prefill kernels hold one block scale per lane (K <= 64 blocks of 128).
 bool prefill_fits(int64_t n, int64_t k, int tables) {
-  return n % prefill_bn(tables) == 0 && k % kScaleBlock == 0 && k / kScaleBlock <= 64 &&
-         (k / kScaleBlock) % kPrefillStages == 0;
+  return n % prefill_bn(tables) == 0 && k % kScaleBlock == 0 && k / kScaleBlock <= 64;
 }
-
 hipError_t launch_grouped_gemm_prefill(const GroupedGemmArgs& a, int tables, int epilogue, hipStream_t stream) {
   if (a.max_tiles <= 0) return hipSuccess;
   if (a.expert_first_tile == nullptr || a.expert_tiles == nullptr) return hipErrorInvalidValue;
@@ -605,9 +604,9 @@ hipError_t launch_grouped_gemm_prefill(const GroupedGemmArgs& a, int tables, int
   if (a.xq != nullptr) {
     if (a.xscale == nullptr) return hipErrorInvalidValue;
     if (tables == 2 && epilogue == kEpiSwiglu)
-      return launch_prefill_fp8<2, 1, 8, kPrefillStages, kEpiSwiglu>(a, stream);
+      return launch_prefill_fp8<2, 1, 8, kEpiSwiglu>(a, stream);
     if (tables == 1 && epilogue == kEpiWeighted)
-      return launch_prefill_fp8<1, 2, 8, kPrefillStages, kEpiWeighted>(a, stream);
+      return launch_prefill_fp8<1, 2, 8, kEpiWeighted>(a, stream);
     return hipErrorInvalidValue;
   }
   if (tables == 2 && epilogue == kEpiSwiglu) return launch_prefill<2, 1, 8, kEpiSwiglu>(a, stream);
