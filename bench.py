@@ -131,6 +131,57 @@ def run_steps(work, steps, warmup, with_stage_events=True):
     return ms, stages, order
 
 
+def full_layer(work, steps, warmup):
+    """The whole MoE layer, as the reference's layer bodies compute it: the bf16
+    shared expert (torch GEMMs on hipBLASLt; random-init N(0, 0.02) weights of
+    the contract's shape, I_shared = 2048) and the routed experts with the
+    epilogue bf16(bf16(routed * 2.5) + shared) fused into their route-sum kernel.
+    Returns (us per layer, algorithmic bytes of the shared expert)."""
+    import torch
+
+    from glm_moe.layers.moe.routed_experts import _shared_swiglu, routed_experts
+
+    cfg = work.cfg
+    device = work.inputs[0][0].device
+    g = torch.Generator(device=device).manual_seed(11)
+    inter_shared = cfg.intermediate  # one shared expert of the routed experts' width (contract local_shared_intermediate x stage_size)
+    sg = (torch.randn((inter_shared, cfg.hidden), generator=g, device=device) * 0.02).to(torch.bfloat16)
+    su = (torch.randn((inter_shared, cfg.hidden), generator=g, device=device) * 0.02).to(torch.bfloat16)
+    sd = (torch.randn((cfg.hidden, inter_shared), generator=g, device=device) * 0.02).to(torch.bfloat16)
+    t = work.tables
+    tables = [t[k] for k in TABLE_KEYS]
+    out = torch.empty((cfg.tokens, cfg.hidden), dtype=torch.bfloat16, device=device)
+    n_rot = len(work.inputs)
+
+    def layer(i):
+        x, ids, w = work.inputs[i % n_rot]
+        shared = _shared_swiglu(x, sg, su, sd)
+        routed_experts(x, ids, w, *tables, out=out, shared=shared, routed_scale=2.5,
+                       activations=work.activations)
+
+    for i in range(warmup):
+        layer(i)
+    start = torch.cuda.Event(enable_timing=True)
+    stop = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record()
+    for i in range(steps):
+        layer(warmup + i)
+    stop.record()
+    torch.cuda.synchronize()
+    shared_bytes = 3 * inter_shared * cfg.hidden * 2
+    return start.elapsed_time(stop) / steps * 1e3, shared_bytes
+
+
+def with_full_layer(s, work, steps):
+    us, shared_bytes = full_layer(work, steps, 3)
+    s["full_layer_us"] = us
+    s["full_layer_hbm_gbs"] = (s["layer_bytes"] + shared_bytes) / (us * 1e-6) / 1e9
+    s["full_layer_note"] = ("routed experts + bf16 shared expert (torch/hipBLASLt) + fused "
+                            "routed*2.5+shared epilogue; value above is the routed experts alone")
+    return s
+
+
 def summarize(work, ms, stages, order):
     gate_up_ms = np.array([s.gate_up for s in stages])
     down_ms = np.array([s.down for s in stages])
@@ -290,6 +341,7 @@ def main():
     head = summarize(work, ms, stages, order)
     head["us_per_layer_with_stage_events"] = ms_ev * 1e3
 
+    with_full_layer(head, work, args.steps)
     roofline = dominant_roofline(cfg, head)
     if args.copy_calibration:
         copy_calibration(device)
@@ -308,6 +360,7 @@ def main():
         s = summarize(swork, sms, sstages, sorder)
         s["hbm_frac"] = s["layer_hbm_gbs"] / HBM_PEAK_GBS
         s["bf16_mfma_frac"] = s["layer_tflops"] / BF16_PEAK_TFLOPS
+        with_full_layer(s, swork, args.secondary_steps)
         if mode == "fp8":
             s["activations"] = "float8_e4m3fn (native FP8 MFMA mode)"
             s["fp8_mfma_frac"] = s["layer_tflops"] / FP8_PEAK_TFLOPS
@@ -341,6 +394,9 @@ def main():
             "tokens": cfg.tokens, "experts": cfg.experts, "hidden": cfg.hidden,
             "intermediate": cfg.intermediate, "top_k": cfg.top_k,
         },
+        "full_layer_us": head["full_layer_us"],
+        "full_layer_hbm_gbs": head["full_layer_hbm_gbs"],
+        "full_layer_note": head["full_layer_note"],
         "layer_hbm_gbs": head["layer_hbm_gbs"],
         "layer_hbm_frac": head["layer_hbm_gbs"] / HBM_PEAK_GBS,
         "stage_us": head["stage_us"],

@@ -82,8 +82,12 @@ __global__ void zero_rows_kernel(uint32_t* out, int64_t rows, int64_t row_words,
 // ids given, a slot whose raw expert id lies outside [0, experts) is not
 // owned and contributes nothing (the decode ownership rule, :250-253).
 // y is [tokens * top_k, h] in flat (token, slot) order.  Eight columns per thread.
+// With shared given, the layer epilogue follows (routed_experts.py:125, :303):
+// out = bf16(bf16(routed * routed_scale) + shared), and any non-finite output
+// clears the health byte (:126); every other health writer ran before.
 __global__ void combine_routes_kernel(const uint16_t* y, int64_t tokens, int32_t top_k, int64_t h,
                                       const int32_t* ids, int32_t experts, int32_t bf16_sum,
+                                      const uint16_t* shared, float routed_scale, uint8_t* valid,
                                       uint16_t* out) {
   const int64_t groups = h / 8;
   const int64_t total = tokens * groups;
@@ -109,6 +113,19 @@ __global__ void combine_routes_kernel(const uint16_t* y, int64_t tokens, int32_t
           }
         }
       }
+    }
+    if (shared != nullptr) {
+      const u32x4 sv = *reinterpret_cast<const u32x4*>(shared + t * h + c);
+      bool finite = true;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        acc[2 * j] = round_to_bf16(round_to_bf16(round_to_bf16(acc[2 * j]) * routed_scale) +
+                                   bf16_bits_to_f32(sv[j] & 0xFFFFu));
+        acc[2 * j + 1] = round_to_bf16(round_to_bf16(round_to_bf16(acc[2 * j + 1]) * routed_scale) +
+                                       bf16_bits_to_f32(sv[j] >> 16));
+        finite &= isfinite(acc[2 * j]) && isfinite(acc[2 * j + 1]);
+      }
+      if (!finite) valid[0] = 0;
     }
     u32x4 o;
 #pragma unroll
@@ -337,12 +354,13 @@ hipError_t launch_zero_rows(void* out, int64_t rows, int64_t row_bytes, const ui
 }
 
 hipError_t launch_combine_routes(const uint16_t* y, int64_t tokens, int32_t top_k, int64_t h,
-                                 const int32_t* ids, int32_t experts, int32_t bf16_sum,
-                                 uint16_t* out, hipStream_t stream) {
+                                 const int32_t* ids, int32_t experts, int32_t bf16_sum, const uint16_t* shared,
+                                 float routed_scale, uint8_t* valid, uint16_t* out, hipStream_t stream) {
   const int64_t total = tokens * (h / 8);
   if (total == 0) return hipSuccess;
+  if (shared != nullptr && valid == nullptr) return hipErrorInvalidValue;
   return launch_kernel(combine_routes_kernel, grid_for(total, 256), dim3(256), 0, stream, y, tokens,
-                     top_k, h, ids, experts, bf16_sum, out);
+                     top_k, h, ids, experts, bf16_sum, shared, routed_scale, valid, out);
 }
 
 hipError_t launch_route_noaux_tc(const float* logits, int64_t tokens, int32_t experts, const float* bias,

@@ -5,6 +5,8 @@
 #include <stdarg.h>
 #include <stdio.h>
 
+#include <cmath>
+#include <cstring>
 #include <string>
 
 #include "../../include/glm_moe.h"
@@ -148,13 +150,24 @@ struct StageTimer {
   }
 };
 
+// RNE float -> bf16 value (finite input): the reference casts the routed scale
+// to bf16 before the epilogue multiply (routed_experts.py:125, :303).
+float bf16_round_host(float f) {
+  uint32_t u;
+  std::memcpy(&u, &f, sizeof(u));
+  u += 0x7FFFu + ((u >> 16) & 1u);
+  u &= 0xFFFF0000u;
+  std::memcpy(&f, &u, sizeof(f));
+  return f;
+}
+
 int routed_experts_impl(const uint16_t* hidden, int64_t tokens, int64_t hidden_size,
                         const int32_t* route_indices, const float* route_weights, int32_t top_k,
                         int32_t num_experts, int64_t intermediate, const uint8_t* gate_bits,
                         const float* gate_scale, const uint8_t* up_bits, const float* up_scale,
                         const uint8_t* down_bits, const float* down_scale, uint32_t flags,
-                        uint16_t* out, uint8_t* valid, void* workspace, size_t workspace_bytes,
-                        const StageTimer& timer, void* stream_ptr) {
+                        const uint16_t* shared, float routed_scale, uint16_t* out, uint8_t* valid,
+                        void* workspace, size_t workspace_bytes, const StageTimer& timer, void* stream_ptr) {
   GLM_REQUIRE(tokens > 0 && top_k > 0 && num_experts > 0, "routed experts need tokens, top_k, experts > 0");
   GLM_REQUIRE(top_k <= num_experts, "top_k exceeds expert count");
   GLM_REQUIRE(num_experts <= kMaxExperts, "at most %d experts", kMaxExperts);
@@ -222,6 +235,8 @@ int routed_experts_impl(const uint16_t* hidden, int64_t tokens, int64_t hidden_s
     d.act = act;
     d.out = out;
     d.valid = valid;
+    d.shared = shared;
+    d.routed_scale = routed_scale;
     const LaunchEvents stage_events[2] = {timer.at(kStageGateUp), timer.at(kStageDown)};
     if (timer.events) *timer.timed = (1u << kStageGateUp) | (1u << kStageDown);
     GLM_HIP(launch_decode_routed(d, stream, timer.events ? stage_events : nullptr), "decode launch");
@@ -329,7 +344,8 @@ int routed_experts_impl(const uint16_t* hidden, int64_t tokens, int64_t hidden_s
   timer.arm(kStageCombine);
   GLM_HIP(launch_combine_routes(y, tokens, top_k, hidden_size,
                                 (flags & GLM_MOE_DROP_UNOWNED) ? route_indices : nullptr, num_experts,
-                                (flags & GLM_MOE_ROUTE_SUM_BF16) ? 1 : 0, out, stream),
+                                (flags & GLM_MOE_ROUTE_SUM_BF16) ? 1 : 0, shared, routed_scale, valid, out,
+                                stream),
           "combine launch");
   timer.done(kStageCombine);
   return GLM_MOE_OK;
@@ -577,7 +593,7 @@ int glm_moe_routed_experts(const uint16_t* hidden, int64_t tokens, int64_t hidde
                            void* stream) {
   return routed_experts_impl(hidden, tokens, hidden_size, route_indices, route_weights, top_k,
                              num_experts, intermediate, gate_bits, gate_scale, up_bits, up_scale,
-                             down_bits, down_scale, flags, out, valid, workspace, workspace_bytes,
+                             down_bits, down_scale, flags, nullptr, 0.0f, out, valid, workspace, workspace_bytes,
                              StageTimer{nullptr, nullptr}, stream);
 }
 
@@ -594,8 +610,22 @@ int glm_moe_routed_experts_timed(const uint16_t* hidden, int64_t tokens, int64_t
   for (int i = 0; i < 2 * kStages; ++i) GLM_REQUIRE(events[i] != nullptr, "eight events required");
   return routed_experts_impl(hidden, tokens, hidden_size, route_indices, route_weights, top_k,
                              num_experts, intermediate, gate_bits, gate_scale, up_bits, up_scale,
-                             down_bits, down_scale, flags, out, valid, workspace, workspace_bytes,
+                             down_bits, down_scale, flags, nullptr, 0.0f, out, valid, workspace, workspace_bytes,
                              StageTimer{events, timed_stages}, stream);
+}
+
+int glm_moe_moe_layer(const uint16_t* hidden, int64_t tokens, int64_t hidden_size, const int32_t* route_indices,
+                      const float* route_weights, int32_t top_k, int32_t num_experts, int64_t intermediate,
+                      const uint8_t* gate_bits, const float* gate_scale, const uint8_t* up_bits,
+                      const float* up_scale, const uint8_t* down_bits, const float* down_scale, uint32_t flags,
+                      const uint16_t* shared, float routed_scale, uint16_t* out, uint8_t* valid, void* workspace,
+                      size_t workspace_bytes, void* stream) {
+  GLM_REQUIRE(shared != nullptr, "null shared-expert rows");
+  GLM_REQUIRE(std::isfinite(routed_scale), "routed scale must be finite");
+  return routed_experts_impl(hidden, tokens, hidden_size, route_indices, route_weights, top_k,
+                             num_experts, intermediate, gate_bits, gate_scale, up_bits, up_scale,
+                             down_bits, down_scale, flags, shared, bf16_round_host(routed_scale), out, valid,
+                             workspace, workspace_bytes, StageTimer{nullptr, nullptr}, stream);
 }
 
 int glm_moe_event_create(void** event) {

@@ -292,6 +292,8 @@ void decode_gate_up_kernel(const DecodeArgs a, int wave_steps) {
   float(*red)[2][kGemvRows] = reinterpret_cast<float(*)[2][kGemvRows]>(smem);
   const int lane = threadIdx.x & 63;
   const int wk = uniform(threadIdx.x >> 6);  // wave-uniform: scalar loop control
+  // health starts true; the down kernel (next on the stream) only clears it
+  if (blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0) a.valid[0] = 1;
   DecodeRoute rt;
   if (!decode_route(a.ids, a.routes, a.experts, a.drop_unowned, blockIdx.x, rt)) return;
   const int I = a.intermediate, H = a.hidden;
@@ -390,7 +392,13 @@ void decode_down_kernel(const DecodeArgs a) {
       sum += res[t * a.top_k + s][row];
       if (a.bf16_sum) sum = round_to_bf16(sum);
     }
-    a.out[(int64_t)t * H + row0 + row] = f32_to_bf16_bits(sum);
+    const int64_t o = (int64_t)t * H + row0 + row;
+    if (a.shared != nullptr) {
+      // layer epilogue (routed_experts.py:125, :303): bf16(bf16(routed * scale) + shared)
+      sum = round_to_bf16(round_to_bf16(round_to_bf16(sum) * a.routed_scale) + bf16_bits_to_f32(a.shared[o]));
+      if (!isfinite(sum)) a.valid[0] = 0;
+    }
+    a.out[o] = f32_to_bf16_bits(sum);
   }
   // health: ids in range, no duplicate id in a row, weights finite and >= 0 if asked
   if (blockIdx.x == 0 && wave == 0) {
@@ -406,7 +414,7 @@ void decode_down_kernel(const DecodeArgs a) {
       }
     }
     const uint64_t any = __ballot(bad);
-    if (lane == 0) a.valid[0] = any ? 0 : 1;
+    if (lane == 0 && any) a.valid[0] = 0;
   }
 }
 

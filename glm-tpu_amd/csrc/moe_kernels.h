@@ -175,6 +175,10 @@ struct DecodeArgs {
   uint16_t* act;               // workspace [routes, intermediate] bf16, flat route order
   uint16_t* out;               // [tokens, hidden] bf16
   uint8_t* valid;
+  // layer epilogue (null shared: out is the routed sum): out = bf16(bf16(routed
+  // * routed_scale) + shared), and health also requires a finite output
+  const uint16_t* shared;      // [tokens, hidden] bf16 shared-expert output
+  float routed_scale;          // already a bf16 value
 };
 // The decode kernels stage one wave's K range (<= 2048) in LDS: hidden <= 8192
 // (four waves split it), intermediate <= 2048.
@@ -197,9 +201,11 @@ hipError_t launch_zero_rows(void* out, int64_t rows, int64_t row_bytes, const ui
                             const uint8_t* valid, hipStream_t stream);
 // out[t] = bf16(sum over slots of y[t * top_k + s]); with ids != nullptr a slot
 // whose raw id is outside [0, experts) contributes nothing (decode ownership).
+// shared: null, or the layer epilogue's bf16 shared-expert rows (out =
+// bf16(bf16(routed * routed_scale) + shared), and a non-finite output clears valid).
 hipError_t launch_combine_routes(const uint16_t* y, int64_t tokens, int32_t top_k, int64_t h,
-                                 const int32_t* ids, int32_t experts, int32_t bf16_sum,
-                                 uint16_t* out, hipStream_t stream);
+                                 const int32_t* ids, int32_t experts, int32_t bf16_sum, const uint16_t* shared,
+                                 float routed_scale, uint8_t* valid, uint16_t* out, hipStream_t stream);
 // GLM noaux_tc routing of [tokens, experts] FP32 logits (experts <= 1024, top_k <= 16).
 hipError_t launch_route_noaux_tc(const float* logits, int64_t tokens, int32_t experts, const float* bias,
                                  int32_t top_k, int32_t* ids, float* weights, hipStream_t stream);

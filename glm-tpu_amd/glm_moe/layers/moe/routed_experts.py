@@ -15,8 +15,9 @@ Work is launched only for the experts the routes select.  On one GPU every
 mesh axis has size 1: ``hidden_local`` is the full hidden state, every expert
 is local and both ``psum`` of the reference are the identity.
 
-The shared expert and ``routed * 2.5 + shared`` use torch bf16 GEMMs on the
-same GPU (hipBLASLt), at the reference's rounding points.
+The shared expert runs as torch bf16 GEMMs on the same GPU (hipBLASLt) at the
+reference's rounding points; the epilogue ``routed * 2.5 + shared`` is fused
+into the library's route-sum kernel (``glm_moe_moe_layer``).
 """
 
 from __future__ import annotations
@@ -189,6 +190,8 @@ def routed_experts(
     activations: str = "bfloat16",
     out: torch.Tensor | None = None,
     events: StageEvents | None = None,
+    shared: torch.Tensor | None = None,
+    routed_scale: float = 2.5,
 ) -> tuple[torch.Tensor, torch.Tensor]:
     """Routed experts of ``[T, H]`` bf16 rows: ``(bf16 [T, H], valid)``.
 
@@ -201,6 +204,11 @@ def routed_experts(
     reference counterpart; prefill shapes only): token rows and SwiGLU
     activations are quantised per (row, 128-wide block) to e4m3 with an FP32
     scale, and the e4m3 x e4m3 block products are scaled in FP32.
+
+    With ``shared`` (the shared expert's bf16 ``[T, H]`` output) the layer
+    epilogue is fused into the kernel that finishes the route sum:
+    ``bf16(bf16(routed * bf16(routed_scale)) + shared)`` (``:125``, ``:303``),
+    and ``valid`` also requires a finite output (``:126``).
     """
     if hidden.ndim != 2 or hidden.dtype != torch.bfloat16:
         raise ValueError("routed experts take bf16 [tokens, hidden] rows")
@@ -224,8 +232,13 @@ def routed_experts(
         raise ValueError("route_sum must be float32 or bfloat16")
     if activations not in ("bfloat16", "float8_e4m3fn"):
         raise ValueError("activations must be bfloat16 or float8_e4m3fn")
+    if shared is not None:
+        if tuple(shared.shape) != (tokens, h) or shared.dtype != torch.bfloat16 or not shared.is_contiguous():
+            raise ValueError("shared expert rows must be contiguous bf16 [tokens, hidden]")
+        if events is not None:
+            raise ValueError("stage events time the routed experts alone")
     _lib.require_device(hidden, route_indices, route_weights, gate_bits, gate_scale, up_bits, up_scale,
-                        down_bits, down_scale, out)
+                        down_bits, down_scale, out, shared)
     device = hidden.device
     if out is None:
         out = torch.empty((tokens, h), dtype=torch.bfloat16, device=device)
@@ -247,7 +260,10 @@ def routed_experts(
         _lib.ptr(gate_bits), _lib.ptr(gate_scale), _lib.ptr(up_bits), _lib.ptr(up_scale), _lib.ptr(down_bits),
         _lib.ptr(down_scale), flags, _lib.ptr(out), _lib.ptr(valid), _lib.ptr(ws), ws.numel(),
     ]
-    if events is None:
+    if shared is not None:
+        args[15:15] = [_lib.ptr(shared), float(routed_scale)]
+        _lib.call("glm_moe_moe_layer", *args, _lib.stream_of(hidden))
+    elif events is None:
         _lib.call("glm_moe_routed_experts", *args, _lib.stream_of(hidden))
     else:
         _lib.call("glm_moe_routed_experts_timed", *args, events.array, ctypes.byref(events.timed),
@@ -326,16 +342,12 @@ def prefill_moe_from_routes(
         or tuple(shared_down_local.shape) != (h, inter)
     ):
         raise ValueError("prefill shared expert geometry differs from contract")
-    routed, valid = routed_experts(
+    shared = _shared_swiglu(hidden_local, shared_gate_local, shared_up_local, shared_down_local)
+    return routed_experts(
         hidden_local, route_indices, route_weights, expert_gate_bits_local, expert_gate_scale_local,
         expert_up_bits_local, expert_up_scale_local, expert_down_bits_local, expert_down_scale_local,
-        route_sum="float32", check_weights=True,
+        route_sum="float32", check_weights=True, shared=shared, routed_scale=contract.routed_scaling_factor,
     )
-    shared = _shared_swiglu(hidden_local, shared_gate_local, shared_up_local, shared_down_local)
-    scale = torch.tensor(contract.routed_scaling_factor, dtype=torch.bfloat16, device=routed.device)
-    output = routed * scale + shared
-    valid = valid & torch.isfinite(output).all()
-    return output, valid
 
 
 def moe_grouped_routes(
@@ -375,11 +387,11 @@ def moe_grouped_routes(
         or tuple(shared_bf16[2].shape) != (h, inter)
     ):
         raise ValueError("grouped MoE BF16 shared tables drifted")
-    routed, _ = routed_experts(
+    shared = _shared_swiglu(hidden_local, *shared_bf16)
+    output, _ = routed_experts(
         hidden_local, route_indices, route_weights, expert_gate_bits_local, expert_gate_scale_local,
         expert_up_bits_local, expert_up_scale_local, expert_down_bits_local, expert_down_scale_local,
-        route_sum="bfloat16", check_weights=False, drop_unowned=True,
+        route_sum="bfloat16", check_weights=False, drop_unowned=True, shared=shared,
+        routed_scale=contract.routed_scaling_factor,
     )
-    shared = _shared_swiglu(hidden_local, *shared_bf16)
-    scale = torch.tensor(contract.routed_scaling_factor, dtype=torch.bfloat16, device=routed.device)
-    return routed * scale + shared
+    return output

@@ -175,6 +175,23 @@ int glm_moe_routed_experts_timed(const uint16_t* hidden, int64_t tokens, int64_t
                                  size_t workspace_bytes, void* const* events, uint32_t* timed_stages,
                                  void* stream);
 
+/* The whole MoE layer output given the shared expert's rows: the routed
+ * experts exactly as glm_moe_routed_experts, then, fused into the kernel that
+ * finishes the route sum, out = bf16(bf16(routed * bf16(routed_scale)) + shared).
+ * Replaces the layer epilogue of prefill_moe_from_routes and moe_grouped_routes
+ * (glm_tpu/layers/moe/routed_experts.py:119-127 and :297-304); the shared
+ * expert itself (bf16 resident GEMMs, :119-124 / :269-302) is the caller's,
+ * e.g. hipBLASLt, and shared holds its bf16 output [tokens, hidden_size].
+ * valid additionally requires every output element to be finite (:126).
+ * Same workspace as glm_moe_routed_experts. */
+int glm_moe_moe_layer(const uint16_t* hidden, int64_t tokens, int64_t hidden_size,
+                      const int32_t* route_indices, const float* route_weights, int32_t top_k,
+                      int32_t num_experts, int64_t intermediate, const uint8_t* gate_bits,
+                      const float* gate_scale, const uint8_t* up_bits, const float* up_scale,
+                      const uint8_t* down_bits, const float* down_scale, uint32_t flags,
+                      const uint16_t* shared, float routed_scale, uint16_t* out, uint8_t* valid,
+                      void* workspace, size_t workspace_bytes, void* stream);
+
 /* Synthetic FP8 expert tables for tests and benchmarks, the reference's fixture
  * recipe (tools/equivalence/fixture.py:158-172) with 128x128 block scales:
  * w ~ N(0, sigma) (counter-based hash + Box-Muller), scale = amax/448 per block,

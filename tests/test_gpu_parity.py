@@ -325,6 +325,55 @@ def test_layers_toy_golden(device, golden):
     print("toy decode layer:", assert_moe_close(host_f32(dec), O.bf16_from_bits(g["decode_layer_bits"])))
 
 
+# ----------------------------------------------------------------------------- fused layer epilogue
+# glm_moe_moe_layer: out = bf16(bf16(routed * bf16(2.5)) + shared), fused into the
+# kernel that finishes the route sum (routed_experts.py:125, :303).  It must equal
+# the same epilogue done by torch bf16 ops after the routed call, bit for bit.
+@pytest.mark.parametrize("tokens,experts,hidden,inter,top_k,route_sum", [
+    (1, 16, 512, 256, 8, "bfloat16"),   # decode kernels, the decode body's bf16 route sum
+    (3, 16, 512, 256, 4, "float32"),    # decode kernels, the prefill body's FP32 route sum
+    (300, 64, 256, 512, 6, "float32"),  # route plan + grouped GEMMs + combine kernel
+    (512, 16, 512, 256, 8, "float32"),  # prefill kernels (wide tiles)
+])
+def test_fused_layer_epilogue_equals_unfused(device, tokens, experts, hidden, inter, top_k, route_sum):
+    from glm_moe.layers.moe.routed_experts import routed_experts
+
+    cfg, x, ids, w, tables = _small_case(tokens, experts, hidden, inter, top_k, 0.0, seed=tokens + 40)
+    t = _device_tables(tables, device)
+    args = (bf16_dev(x, device), dev(ids, device), dev(w, device), *(t[k] for k in TABLE_KEYS))
+    rng = np.random.default_rng(tokens)
+    shared_f32 = (rng.standard_normal((tokens, hidden)) * 0.05).astype(np.float32)
+    shared = bf16_dev(shared_f32, device)
+    routed, ok = routed_experts(*args, route_sum=route_sum)
+    want = routed * torch.tensor(2.5, dtype=torch.bfloat16, device=device) + shared
+    got, ok_fused = routed_experts(*args, route_sum=route_sum, shared=shared, routed_scale=2.5)
+    assert bool(ok) and bool(ok_fused)
+    np.testing.assert_array_equal(bf16_bits_of(got), bf16_bits_of(want))
+    # and against the oracle's layer epilogue on its own routed output
+    ref_routed, _ = O.routed_experts(x, ids, w, **tables, route_sum=route_sum)
+    ref = O.bf16_round(O.bf16_round(ref_routed * np.float32(2.5)) + O.bf16_round(shared_f32))
+    print(cfg, assert_moe_close(host_f32(got), ref))
+
+
+@pytest.mark.parametrize("tokens,top_k", [(2, 4), (300, 4)])  # decode kernels / combine kernel
+def test_fused_layer_nonfinite_output_clears_health(device, tokens, top_k):
+    from glm_moe.layers.moe.routed_experts import routed_experts
+
+    cfg, x, ids, w, tables = _small_case(tokens, 16, 512, 256, top_k, 0.0, seed=7)
+    t = _device_tables(tables, device)
+    args = (bf16_dev(x, device), dev(ids, device), dev(w, device), *(t[k] for k in TABLE_KEYS))
+    shared = torch.zeros((tokens, 512), dtype=torch.bfloat16, device=device)
+    _, ok = routed_experts(*args, shared=shared)
+    assert bool(ok)
+    shared[tokens - 1, 300] = float("inf")
+    out, ok = routed_experts(*args, shared=shared)
+    assert not bool(ok)  # routed_experts.py:126: the output must be finite
+    assert torch.isinf(out[tokens - 1, 300].float())
+    shared[tokens - 1, 300] = 0.0
+    _, ok = routed_experts(*args, shared=shared)
+    assert bool(ok)  # health is recomputed on every call
+
+
 def _small_case(tokens, experts, hidden, inter, top_k, zipf, seed):
     from glm_moe import synthetic as S
 

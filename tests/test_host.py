@@ -98,6 +98,14 @@ def test_static_refusals_raise_value_error_through_the_abi():
     assert status == _lib.ERR_ARGUMENT
     with pytest.raises(ValueError, match="FP8 activations need a prefill shape"):
         _lib.check(status)
+    # the fused layer epilogue needs the shared-expert rows and a finite scale
+    status = lib.glm_moe_moe_layer(fake, 1, 6144, fake, fake, 8, 256, 2048, fake, fake, fake, fake, fake, fake, 0,
+                                   null, ctypes.c_float(2.5), fake, fake, fake, 1 << 30, null)
+    assert status == _lib.ERR_ARGUMENT
+    status = lib.glm_moe_moe_layer(fake, 1, 6144, fake, fake, 8, 256, 2048, fake, fake, fake, fake, fake, fake, 0,
+                                   fake, ctypes.c_float(float("inf")), fake, fake, fake, 1 << 30, null)
+    with pytest.raises(ValueError, match="routed scale must be finite"):
+        _lib.check(status)
 
 
 def test_python_api_refuses_bad_geometry_and_cpu_tensors():
@@ -131,6 +139,11 @@ def test_python_api_refuses_bad_geometry_and_cpu_tensors():
     with pytest.raises(ValueError, match="bf16"):
         routed_experts(lhs.float(), torch.zeros((8, 2), dtype=torch.int32), torch.zeros((8, 2)), bits, scale,
                        bits, scale, bits, scale)
+    ids2, w2 = torch.zeros((8, 2), dtype=torch.int32), torch.zeros((8, 2))
+    with pytest.raises(ValueError, match="shared expert rows"):
+        routed_experts(lhs, ids2, w2, bits, scale, bits, scale, bits, scale, shared=lhs[:4])
+    with pytest.raises(ValueError, match="shared expert rows"):
+        routed_experts(lhs, ids2, w2, bits, scale, bits, scale, bits, scale, shared=lhs.float())
 
 
 def test_contract_mirrors_the_reference():
