@@ -305,6 +305,30 @@ dim3 grid_for(int64_t work, int threads) {
   return dim3((unsigned)blocks);
 }
 
+// Count of e4m3fn NaN encodings (0x7F, 0xFF) in n bytes, added to *count:
+// the checkpoint's finite-bit gate (glm_tpu/model_loader/sharded_state/
+// format.py:307-315).  Four bytes a lane per 32-bit word: a byte b is NaN iff
+// (b & 0x7F) == 0x7F, found for all four at once with the zero-byte trick on
+// (w & 0x7F7F7F7F) ^ 0x7F7F7F7F.  Per-wave sums, one global atomic per wave.
+__global__ void count_nonfinite_fp8_kernel(const uint8_t* bits, int64_t n, unsigned long long* count) {
+  const int64_t words = n >> 2;
+  const uint32_t* w32 = reinterpret_cast<const uint32_t*>(bits);
+  unsigned long long local = 0;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < words;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const uint32_t x = (w32[i] & 0x7F7F7F7Fu) ^ 0x7F7F7F7Fu;
+    // exact per-byte zero test: bit 7 of each byte of ~(((x & 0x7F..) + 0x7F..) | x) is set iff that byte is 0
+    const uint32_t z = ~(((x & 0x7F7F7F7Fu) + 0x7F7F7F7Fu) | x | 0x7F7F7F7Fu);
+    local += (unsigned long long)__popc(z);
+  }
+  if (blockIdx.x == 0 && threadIdx.x < (n & 3)) {
+    const uint8_t b = bits[(words << 2) + threadIdx.x];
+    local += (b & 0x7F) == 0x7F ? 1ull : 0ull;
+  }
+  for (int off = 32; off > 0; off >>= 1) local += __shfl_xor(local, off, 64);
+  if ((threadIdx.x & 63) == 0 && local != 0) atomicAdd(count, local);
+}
+
 }  // namespace
 
 hipError_t launch_synth_fp8(uint64_t seed, int32_t experts, int64_t n, int64_t k, float sigma,
@@ -361,6 +385,14 @@ hipError_t launch_combine_routes(const uint16_t* y, int64_t tokens, int32_t top_
   if (shared != nullptr && valid == nullptr) return hipErrorInvalidValue;
   return launch_kernel(combine_routes_kernel, grid_for(total, 256), dim3(256), 0, stream, y, tokens,
                      top_k, h, ids, experts, bf16_sum, shared, routed_scale, valid, out);
+}
+
+hipError_t launch_count_nonfinite_fp8(const uint8_t* bits, int64_t n, unsigned long long* count,
+                                      hipStream_t stream) {
+  if (n <= 0) return hipSuccess;
+  const int64_t words = (n >> 2) > 0 ? (n >> 2) : 1;
+  const int64_t blocks = words / 256 + 1 < 4096 ? words / 256 + 1 : 4096;
+  return launch_kernel(count_nonfinite_fp8_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, bits, n, count);
 }
 
 hipError_t launch_route_noaux_tc(const float* logits, int64_t tokens, int32_t experts, const float* bias,

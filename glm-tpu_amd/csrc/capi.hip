@@ -383,6 +383,17 @@ int glm_moe_route_noaux_tc(const float* router_logits, int64_t tokens, int32_t n
   return GLM_MOE_OK;
 }
 
+int glm_moe_count_nonfinite_fp8(const uint8_t* bits, int64_t n, uint64_t* count, void* stream) {
+  GLM_REQUIRE(n >= 0, "byte count must be >= 0");
+  if (n == 0) return GLM_MOE_OK;
+  GLM_REQUIRE(bits && count, "null tensor pointer");
+  GLM_REQUIRE(reinterpret_cast<uintptr_t>(bits) % 4 == 0 && reinterpret_cast<uintptr_t>(count) % 8 == 0,
+              "FP8 bytes must be 4-byte aligned and the count 8-byte aligned");
+  GLM_HIP(launch_count_nonfinite_fp8(bits, n, reinterpret_cast<unsigned long long*>(count), as_stream(stream)),
+          "finite-bit scan launch");
+  return GLM_MOE_OK;
+}
+
 int glm_moe_group_routes(const int32_t* route_indices, int64_t tokens, int32_t top_k,
                          int32_t num_experts, int32_t* sorted_flat_ids,
                          int32_t* inverse_permutation, int32_t* group_sizes, uint8_t* valid,

@@ -207,6 +207,9 @@ hipError_t launch_combine_routes(const uint16_t* y, int64_t tokens, int32_t top_
                                  const int32_t* ids, int32_t experts, int32_t bf16_sum, const uint16_t* shared,
                                  float routed_scale, uint8_t* valid, uint16_t* out, hipStream_t stream);
 // GLM noaux_tc routing of [tokens, experts] FP32 logits (experts <= 1024, top_k <= 16).
+// Adds the count of e4m3fn NaN bytes (0x7F / 0xFF) among n bytes to *count.
+hipError_t launch_count_nonfinite_fp8(const uint8_t* bits, int64_t n, unsigned long long* count,
+                                      hipStream_t stream);
 hipError_t launch_route_noaux_tc(const float* logits, int64_t tokens, int32_t experts, const float* bias,
                                  int32_t top_k, int32_t* ids, float* weights, hipStream_t stream);
 // Per (row, 128-wide block): scale = amax / 448 (1 for an all-zero block),

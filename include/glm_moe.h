@@ -63,6 +63,14 @@ const char* glm_moe_last_error(void);
 int glm_moe_decode_fp8_table(const uint8_t* bits, const float* scale, int64_t n, int64_t k,
                              int32_t block_n, int32_t block_k, uint16_t* out_bf16, void* stream);
 
+/* Finite-bit gate of FP8 checkpoint payloads: adds to *count (device uint64)
+ * the number of e4m3fn NaN encodings (0x7F, 0xFF) among n bytes; a loader
+ * refuses any payload with a non-zero count.  Replaces the U8 branch of
+ * _validate_finite_chunk (glm_tpu/model_loader/sharded_state/format.py:307-315),
+ * run on the GPU over tables already in HBM.  The caller zeroes *count; bits
+ * must be 4-byte aligned. */
+int glm_moe_count_nonfinite_fp8(const uint8_t* bits, int64_t n, uint64_t* count, void* stream);
+
 /* Replaces glm_tpu/layers/moe/router.py:20-55 route_glm_noaux_tc_logits: FP32
  * sigmoid scores of logits [tokens, experts]; the top_k experts of scores + bias
  * (bias may be NULL: zero), best first, ties to the lowest id; weights = the
