@@ -214,8 +214,8 @@ DECODE_PATH_MAX_ROUTES = 64  # routes handled by the two decode GEMV kernels (li
 # 1 GiB copy calibration of `bench.py --copy-calibration`); the command and the
 # raw counter summary are in the named profile.
 MEASURED_TRAFFIC = {
-    ("decode_t1", "decode_gate_up_kernel"): {"bytes": 201.79e6, "source": "profiles/decode_t1_hbm_traffic.md"},
-    ("prefill_t2048", "prefill_gemm_kernel"): {"bytes": 6888.0e6, "source": "profiles/prefill_t2048_hbm_traffic.md"},
+    ("decode_t1", "decode_gate_up_kernel"): {"bytes": 201.80e6, "source": "profiles/decode_t1_hbm_traffic.md"},
+    ("prefill_t2048", "prefill_gemm_kernel"): {"bytes": 6700.1e6, "source": "profiles/prefill_t2048_hbm_traffic.md"},
 }
 
 
