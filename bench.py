@@ -133,13 +133,15 @@ def run_steps(work, steps, warmup, with_stage_events=True):
 
 def full_layer(work, steps, warmup):
     """The whole MoE layer, as the reference's layer bodies compute it: the bf16
-    shared expert (torch GEMMs on hipBLASLt; random-init N(0, 0.02) weights of
-    the contract's shape, I_shared = 2048) and the routed experts with the
-    epilogue bf16(bf16(routed * 2.5) + shared) fused into their route-sum kernel.
-    Returns (us per layer, algorithmic bytes of the shared expert)."""
+    shared expert (random-init N(0, 0.02) weights of the contract's shape,
+    I_shared = I) and the routed experts with the epilogue
+    bf16(bf16(routed * 2.5) + shared) fused into their route-sum kernel.  On
+    decode shapes the shared expert runs inside the two decode kernels
+    (glm_moe_moe_layer_resident), else as torch GEMMs on hipBLASLt.
+    Returns (us per layer, algorithmic bytes of the shared expert, how)."""
     import torch
 
-    from glm_moe.layers.moe.routed_experts import _shared_swiglu, routed_experts
+    from glm_moe.layers.moe.routed_experts import _shared_swiglu, routed_experts, uses_decode_kernels
 
     cfg = work.cfg
     device = work.inputs[0][0].device
@@ -153,11 +155,19 @@ def full_layer(work, steps, warmup):
     out = torch.empty((cfg.tokens, cfg.hidden), dtype=torch.bfloat16, device=device)
     n_rot = len(work.inputs)
 
+    # one row (the decode body): the shared expert inside the decode kernels; more
+    # rows: hipBLASLt, which reads the shared weights once for all of them
+    resident = work.activations == "bfloat16" and cfg.tokens == 1 and uses_decode_kernels(
+        1, cfg.top_k, cfg.hidden, cfg.intermediate)
+
     def layer(i):
         x, ids, w = work.inputs[i % n_rot]
-        shared = _shared_swiglu(x, sg, su, sd)
-        routed_experts(x, ids, w, *tables, out=out, shared=shared, routed_scale=2.5,
-                       activations=work.activations)
+        if resident:
+            routed_experts(x, ids, w, *tables, out=out, shared_tables=(sg, su, sd), routed_scale=2.5)
+        else:
+            shared = _shared_swiglu(x, sg, su, sd)
+            routed_experts(x, ids, w, *tables, out=out, shared=shared, routed_scale=2.5,
+                           activations=work.activations)
 
     for i in range(warmup):
         layer(i)
@@ -170,15 +180,16 @@ def full_layer(work, steps, warmup):
     stop.record()
     torch.cuda.synchronize()
     shared_bytes = 3 * inter_shared * cfg.hidden * 2
-    return start.elapsed_time(stop) / steps * 1e3, shared_bytes
+    how = ("shared expert inside the two decode kernels (glm_moe_moe_layer_resident)" if resident else
+           "shared expert on torch/hipBLASLt, epilogue fused (glm_moe_moe_layer)")
+    return start.elapsed_time(stop) / steps * 1e3, shared_bytes, how
 
 
 def with_full_layer(s, work, steps):
-    us, shared_bytes = full_layer(work, steps, 3)
+    us, shared_bytes, how = full_layer(work, steps, 3)
     s["full_layer_us"] = us
     s["full_layer_hbm_gbs"] = (s["layer_bytes"] + shared_bytes) / (us * 1e-6) / 1e9
-    s["full_layer_note"] = ("routed experts + bf16 shared expert (torch/hipBLASLt) + fused "
-                            "routed*2.5+shared epilogue; value above is the routed experts alone")
+    s["full_layer_note"] = f"routed experts + bf16 shared expert + fused routed*2.5+shared epilogue; {how}"
     return s
 
 

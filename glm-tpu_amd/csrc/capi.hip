@@ -84,7 +84,7 @@ bool uses_decode_path(int64_t routes, int64_t hidden, int64_t intermediate) {
 // Byte layout of the glm_moe_routed_experts workspace.
 struct RoutedLayout {
   size_t sorted, inverse, counts, offsets, tiles, expert_tiles, chunk_hist, chunk_bad, act, y, xq, xscale, actq,
-      actscale, total;
+      actscale, act_shared, total;
   int64_t max_tiles;
 };
 
@@ -111,6 +111,8 @@ RoutedLayout routed_layout(int64_t tokens, int32_t top_k, int32_t experts, int64
   L.xscale = off;   off = align_up(off + sizeof(float) * tokens * (hidden / 128));
   L.actq = off;     off = align_up(off + (size_t)n * intermediate);
   L.actscale = off; off = align_up(off + sizeof(float) * n * (intermediate / 128));
+  // resident shared expert (decode shapes): its bf16 SwiGLU activations
+  L.act_shared = off; off = align_up(off + sizeof(uint16_t) * tokens * intermediate);
   L.total = off;
   return L;
 }
@@ -166,8 +168,9 @@ int routed_experts_impl(const uint16_t* hidden, int64_t tokens, int64_t hidden_s
                         int32_t num_experts, int64_t intermediate, const uint8_t* gate_bits,
                         const float* gate_scale, const uint8_t* up_bits, const float* up_scale,
                         const uint8_t* down_bits, const float* down_scale, uint32_t flags,
-                        const uint16_t* shared, float routed_scale, uint16_t* out, uint8_t* valid,
-                        void* workspace, size_t workspace_bytes, const StageTimer& timer, void* stream_ptr) {
+                        const uint16_t* shared, const uint16_t* const* resident, float routed_scale,
+                        uint16_t* out, uint8_t* valid, void* workspace, size_t workspace_bytes,
+                        const StageTimer& timer, void* stream_ptr) {
   GLM_REQUIRE(tokens > 0 && top_k > 0 && num_experts > 0, "routed experts need tokens, top_k, experts > 0");
   GLM_REQUIRE(top_k <= num_experts, "top_k exceeds expert count");
   GLM_REQUIRE(num_experts <= kMaxExperts, "at most %d experts", kMaxExperts);
@@ -237,12 +240,22 @@ int routed_experts_impl(const uint16_t* hidden, int64_t tokens, int64_t hidden_s
     d.valid = valid;
     d.shared = shared;
     d.routed_scale = routed_scale;
+    if (resident != nullptr) {
+      d.shared_gate = resident[0];
+      d.shared_up = resident[1];
+      d.shared_down = resident[2];
+      d.act_shared = reinterpret_cast<uint16_t*>(ws + L.act_shared);
+    }
     const LaunchEvents stage_events[2] = {timer.at(kStageGateUp), timer.at(kStageDown)};
     if (timer.events) *timer.timed = (1u << kStageGateUp) | (1u << kStageDown);
     GLM_HIP(launch_decode_routed(d, stream, timer.events ? stage_events : nullptr), "decode launch");
     return GLM_MOE_OK;
   }
 
+  GLM_REQUIRE(resident == nullptr,
+              "the resident shared expert runs on decode shapes (at most %d routes); pass the shared "
+              "expert's output to glm_moe_moe_layer instead",
+              kMaxDecodeRoutes);
   RoutePlanArgs p{};
   p.ids = route_indices;
   p.n = (int32_t)n;
@@ -604,7 +617,7 @@ int glm_moe_routed_experts(const uint16_t* hidden, int64_t tokens, int64_t hidde
                            void* stream) {
   return routed_experts_impl(hidden, tokens, hidden_size, route_indices, route_weights, top_k,
                              num_experts, intermediate, gate_bits, gate_scale, up_bits, up_scale,
-                             down_bits, down_scale, flags, nullptr, 0.0f, out, valid, workspace, workspace_bytes,
+                             down_bits, down_scale, flags, nullptr, nullptr, 0.0f, out, valid, workspace, workspace_bytes,
                              StageTimer{nullptr, nullptr}, stream);
 }
 
@@ -621,7 +634,7 @@ int glm_moe_routed_experts_timed(const uint16_t* hidden, int64_t tokens, int64_t
   for (int i = 0; i < 2 * kStages; ++i) GLM_REQUIRE(events[i] != nullptr, "eight events required");
   return routed_experts_impl(hidden, tokens, hidden_size, route_indices, route_weights, top_k,
                              num_experts, intermediate, gate_bits, gate_scale, up_bits, up_scale,
-                             down_bits, down_scale, flags, nullptr, 0.0f, out, valid, workspace, workspace_bytes,
+                             down_bits, down_scale, flags, nullptr, nullptr, 0.0f, out, valid, workspace, workspace_bytes,
                              StageTimer{events, timed_stages}, stream);
 }
 
@@ -635,8 +648,40 @@ int glm_moe_moe_layer(const uint16_t* hidden, int64_t tokens, int64_t hidden_siz
   GLM_REQUIRE(std::isfinite(routed_scale), "routed scale must be finite");
   return routed_experts_impl(hidden, tokens, hidden_size, route_indices, route_weights, top_k,
                              num_experts, intermediate, gate_bits, gate_scale, up_bits, up_scale,
-                             down_bits, down_scale, flags, shared, bf16_round_host(routed_scale), out, valid,
-                             workspace, workspace_bytes, StageTimer{nullptr, nullptr}, stream);
+                             down_bits, down_scale, flags, shared, nullptr, bf16_round_host(routed_scale), out,
+                             valid, workspace, workspace_bytes, StageTimer{nullptr, nullptr}, stream);
+}
+
+int glm_moe_uses_decode_kernels(int64_t tokens, int32_t top_k, int64_t hidden_size, int64_t intermediate) {
+  return tokens > 0 && top_k > 0 && hidden_size > 0 && intermediate > 0 &&
+                 uses_decode_path(tokens * top_k, hidden_size, intermediate)
+             ? 1
+             : 0;
+}
+
+int glm_moe_moe_layer_resident(const uint16_t* hidden, int64_t tokens, int64_t hidden_size,
+                               const int32_t* route_indices, const float* route_weights, int32_t top_k,
+                               int32_t num_experts, int64_t intermediate, const uint8_t* gate_bits,
+                               const float* gate_scale, const uint8_t* up_bits, const float* up_scale,
+                               const uint8_t* down_bits, const float* down_scale, uint32_t flags,
+                               const uint16_t* shared_gate, const uint16_t* shared_up, const uint16_t* shared_down,
+                               int64_t shared_intermediate, float routed_scale, uint16_t* out, uint8_t* valid,
+                               void* workspace, size_t workspace_bytes, void* stream) {
+  GLM_REQUIRE(shared_gate && shared_up && shared_down, "null shared-expert table");
+  GLM_REQUIRE(shared_intermediate == intermediate,
+              "the resident shared expert needs the routed experts' intermediate size (%lld), got %lld",
+              (long long)intermediate, (long long)shared_intermediate);
+  GLM_REQUIRE(std::isfinite(routed_scale), "routed scale must be finite");
+  GLM_REQUIRE((flags & GLM_MOE_FP8_ACTIVATIONS) == 0, "the resident shared expert takes bf16 activations");
+  GLM_REQUIRE(tokens > 0 && top_k > 0 && uses_decode_path(tokens * top_k, hidden_size, intermediate),
+              "the resident shared expert runs on decode shapes (at most %d routes); pass the shared "
+              "expert's output to glm_moe_moe_layer instead",
+              kMaxDecodeRoutes);
+  const uint16_t* resident[3] = {shared_gate, shared_up, shared_down};
+  return routed_experts_impl(hidden, tokens, hidden_size, route_indices, route_weights, top_k,
+                             num_experts, intermediate, gate_bits, gate_scale, up_bits, up_scale,
+                             down_bits, down_scale, flags, nullptr, resident, bf16_round_host(routed_scale), out,
+                             valid, workspace, workspace_bytes, StageTimer{nullptr, nullptr}, stream);
 }
 
 int glm_moe_event_create(void** event) {

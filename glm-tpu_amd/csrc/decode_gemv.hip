@@ -85,6 +85,15 @@ __device__ __forceinline__ bool decode_route(const int32_t* ids, int n, int expe
   return true;
 }
 
+// The number of active routes (those decode_route enumerates), wave-uniform.
+__device__ __forceinline__ int decode_active_routes(const int32_t* ids, int n, int experts, bool drop_unowned) {
+  const int lane = threadIdx.x & 63;
+  const int raw = lane < n ? ids[lane] : -1;
+  const bool owned = raw >= 0 && raw < experts;
+  const bool active = lane < n && (owned || !drop_unowned);
+  return __popcll(__ballot(active));
+}
+
 // The K range [step_begin, step_end) of one wave over TABLES tables of the
 // same 16 rows, against one route's activations.
 template <int TABLES>
@@ -284,6 +293,98 @@ __device__ __forceinline__ float sum16(float v) {
 
 __host__ __device__ constexpr int xs_elems(int wave_steps) { return wave_steps * kStepK + 16; }
 
+// ------------------------------------------------------------------ bf16 weights (resident shared expert)
+// The same 16-row streams over bf16 tables: a step is still 256 bytes of a row
+// (4 rows x 256 B per load instruction), now 128 K; products are exact bf16 x
+// bf16 in v_dot2c_f32_bf16 with FP32 sums, as the reference's resident_matmul
+// (glm_tpu/layers/linear.py:26-33).  K is a multiple of 128 (whole steps).
+constexpr int kBf16StepK = kStepK / 2;
+
+template <int TABLES>
+struct Bf16Stream {
+  __amdgpu_buffer_rsrc_t w[TABLES];
+  uint32_t lane_off;   // (lane/16) * row_bytes + (lane%16) * 16
+  int row_bytes;       // 2 k
+  int k;
+  int step_begin, step_end;  // steps of 128 elements
+  const uint16_t* x;   // activation row (bf16, k entries)
+  uint16_t* xs;        // the wave's LDS region (the K range)
+};
+
+template <int TABLES>
+__device__ __forceinline__ void bf16_load(const Bf16Stream<TABLES>& g, int s, u32x4 (&w)[TABLES][4]) {
+  const uint32_t off = g.lane_off + s * kStepK;
+#pragma unroll
+  for (int t = 0; t < TABLES; ++t)
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      w[t][q] = __builtin_bit_cast(
+          u32x4, __builtin_amdgcn_raw_buffer_load_b128(g.w[t], off, 4 * q * g.row_bytes + g.step_begin * kStepK,
+                                                       kNonTemporal));
+}
+
+template <int TABLES>
+__device__ __forceinline__ void bf16_fma(const Bf16Stream<TABLES>& g, const u32x4 (&w)[TABLES][4], int s, int lane,
+                                         float (&acc)[TABLES][4]) {
+  const u32x4 x = *reinterpret_cast<const u32x4*>(g.xs + s * kBf16StepK + (lane & 15) * 8);
+#pragma unroll
+  for (int t = 0; t < TABLES; ++t)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      float a = acc[t][q];
+#pragma unroll
+      for (int h = 0; h < 4; ++h) {
+        const uint32_t wv = w[t][q][h], xv = x[h];
+        a = __builtin_amdgcn_fdot2_f32_bf16(as_bf16x2(wv), as_bf16x2(xv), a, false);
+      }
+      acc[t][q] = a;
+    }
+}
+
+// The wave's K range with DEPTH steps of weights in flight; the activations
+// are staged once into the wave's LDS region (loads issued before the weights).
+template <int DEPTH, int TABLES>
+__device__ __forceinline__ void bf16_run(const Bf16Stream<TABLES>& g, int lane, float (&acc)[TABLES][4]) {
+  const int n = g.step_end - g.step_begin;
+  if (n <= 0) return;
+  const int last = n - 1;
+  const int kbeg = g.step_begin * kBf16StepK;
+  const int chunks = (n * kBf16StepK) >> 3;  // 8 bf16 a chunk, at most 256
+  u32x4 xv[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int c = lane + 64 * i;
+    if (c < chunks) xv[i] = *reinterpret_cast<const u32x4*>(g.x + kbeg + 8 * c);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  u32x4 ring[DEPTH][TABLES][4];
+#pragma unroll
+  for (int d = 0; d < DEPTH; ++d) {
+    bf16_load(g, min(d, last), ring[d]);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int c = lane + 64 * i;
+    if (c < chunks) *reinterpret_cast<u32x4*>(g.xs + 8 * c) = xv[i];
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  for (int s = 0; s < n; s += DEPTH) {
+#pragma unroll
+    for (int d = 0; d < DEPTH; ++d) {
+      if (s + d < n) bf16_fma(g, ring[d], s + d, lane, acc);
+      __builtin_amdgcn_sched_barrier(0);
+      bf16_load(g, min(s + d + DEPTH, last), ring[d]);
+    }
+  }
+}
+
+// LDS elements a wave's staging region needs for K range `wave_steps` steps of
+// e4m3 (256 K each) or the same range in bf16 steps.
+__host__ __device__ constexpr int bf16_wave_steps(int k, int waves) {
+  return ((k / kBf16StepK) + waves - 1) / waves;
+}
+
 // ------------------------------------------------------------------ gate/up + SwiGLU
 template <int WK>
 __global__ __launch_bounds__(64 * WK) __attribute__((amdgpu_waves_per_eu(4)))
@@ -294,10 +395,46 @@ void decode_gate_up_kernel(const DecodeArgs a, int wave_steps) {
   const int wk = uniform(threadIdx.x >> 6);  // wave-uniform: scalar loop control
   // health starts true; the down kernel (next on the stream) only clears it
   if (blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0) a.valid[0] = 1;
-  DecodeRoute rt;
-  if (!decode_route(a.ids, a.routes, a.experts, a.drop_unowned, blockIdx.x, rt)) return;
   const int I = a.intermediate, H = a.hidden;
   const int row0 = blockIdx.y * kGemvRows;
+  if ((int)blockIdx.x >= a.routes) {
+    // the resident shared expert of token blockIdx.x - routes: bf16 gate/up + SwiGLU
+    const int t = blockIdx.x - a.routes;
+    const int ws = bf16_wave_steps(H, WK);
+    Bf16Stream<2> g;
+    g.k = H;
+    g.row_bytes = 2 * H;
+    g.lane_off = (uint32_t)((lane >> 4) * 2 * H + (lane & 15) * 16);
+    g.step_begin = min(wk * ws, H / kBf16StepK);
+    g.step_end = min(g.step_begin + ws, H / kBf16StepK);
+    g.w[0] = rows_buffer(reinterpret_cast<const uint8_t*>(a.shared_gate + (int64_t)row0 * H), (int64_t)kGemvRows * 2 * H);
+    g.w[1] = rows_buffer(reinterpret_cast<const uint8_t*>(a.shared_up + (int64_t)row0 * H), (int64_t)kGemvRows * 2 * H);
+    g.x = a.hidden_in + (int64_t)t * H;
+    g.xs = reinterpret_cast<uint16_t*>(smem + sizeof(float) * WK * 2 * kGemvRows) + wk * xs_elems(wave_steps);
+    float acc[2][4] = {};
+    bf16_run<kGateUpDepth>(g, lane, acc);
+#pragma unroll
+    for (int tb = 0; tb < 2; ++tb)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const float v = sum16(acc[tb][q]);
+        if ((lane & 15) == 0) red[wk][tb][4 * q + (lane >> 4)] = v;
+      }
+    __syncthreads();
+    const int tid = threadIdx.x;
+    if (tid < kGemvRows) {
+      float gsum = 0.f, usum = 0.f;
+      for (int w = 0; w < WK; ++w) {
+        gsum += red[w][0][tid];
+        usum += red[w][1][tid];
+      }
+      const float v = swiglu_bf16(round_to_bf16(gsum), round_to_bf16(usum));
+      a.act_shared[(int64_t)t * I + row0 + tid] = f32_to_bf16_bits(v);
+    }
+    return;
+  }
+  DecodeRoute rt;
+  if (!decode_route(a.ids, a.routes, a.experts, a.drop_unowned, blockIdx.x, rt)) return;
   const int steps = (H + kStepK - 1) / kStepK;
   GemvStream<2> g;
   g.k = H;
@@ -356,7 +493,35 @@ void decode_down_kernel(const DecodeArgs a) {
   __syncthreads();
   uint16_t* xs = reinterpret_cast<uint16_t*>(smem + sizeof(float) * kMaxDecodeRoutes * kGemvRows) +
                  wave * xs_elems(steps);
-  for (int j = wave;; j += WAVES) {
+  // [tokens][16] bf16 shared-expert down rows, after every wave's staging region
+  float(*res_sh)[kGemvRows] = reinterpret_cast<float(*)[kGemvRows]>(
+      smem + sizeof(float) * kMaxDecodeRoutes * kGemvRows + sizeof(uint16_t) * WAVES * xs_elems(steps));
+  const int tokens = a.routes / a.top_k;
+  const int active = decode_active_routes(a.ids, a.routes, a.experts, a.drop_unowned);
+  const int jobs = active + (a.shared_gate != nullptr ? tokens : 0);
+  for (int j = wave; j < jobs; j += WAVES) {
+    if (j >= active) {
+      // the resident shared expert's down projection of token j - active (bf16, unweighted)
+      const int t = j - active;
+      Bf16Stream<1> g;
+      g.k = I;
+      g.row_bytes = 2 * I;
+      g.lane_off = (uint32_t)((lane >> 4) * 2 * I + (lane & 15) * 16);
+      g.step_begin = 0;
+      g.step_end = I / kBf16StepK;
+      g.w[0] = rows_buffer(reinterpret_cast<const uint8_t*>(a.shared_down + (int64_t)row0 * I),
+                           (int64_t)kGemvRows * 2 * I);
+      g.x = a.act_shared + (int64_t)t * I;
+      g.xs = xs;
+      float acc[1][4] = {};
+      bf16_run<kDownDepth>(g, lane, acc);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const float v = sum16(acc[0][q]);
+        if ((lane & 15) == 0) res_sh[t][4 * q + (lane >> 4)] = round_to_bf16(v);
+      }
+      continue;
+    }
     DecodeRoute rt;
     if (!decode_route(a.ids, a.routes, a.experts, a.drop_unowned, j, rt)) break;
     GemvStream<1> g;
@@ -384,7 +549,6 @@ void decode_down_kernel(const DecodeArgs a) {
   }
   __syncthreads();
   // route combine: every token's slots in slot order, FP32 (or bf16 running) sum
-  const int tokens = a.routes / a.top_k;
   for (int i = tid; i < tokens * kGemvRows; i += 64 * WAVES) {
     const int t = i / kGemvRows, row = i % kGemvRows;
     float sum = 0.f;
@@ -393,7 +557,11 @@ void decode_down_kernel(const DecodeArgs a) {
       if (a.bf16_sum) sum = round_to_bf16(sum);
     }
     const int64_t o = (int64_t)t * H + row0 + row;
-    if (a.shared != nullptr) {
+    if (a.shared_gate != nullptr) {
+      // layer epilogue with the resident shared expert computed above
+      sum = round_to_bf16(round_to_bf16(round_to_bf16(sum) * a.routed_scale) + res_sh[t][row]);
+      if (!isfinite(sum)) a.valid[0] = 0;
+    } else if (a.shared != nullptr) {
       // layer epilogue (routed_experts.py:125, :303): bf16(bf16(routed * scale) + shared)
       sum = round_to_bf16(round_to_bf16(round_to_bf16(sum) * a.routed_scale) + bf16_bits_to_f32(a.shared[o]));
       if (!isfinite(sum)) a.valid[0] = 0;
@@ -438,14 +606,21 @@ hipError_t launch_decode_routed(const DecodeArgs& a, hipStream_t stream, const L
   const int gu_steps = gate_up_wave_steps(a.hidden);
   const size_t gu_lds = sizeof(float) * kGateUpWaves * 2 * kGemvRows +
                         sizeof(uint16_t) * kGateUpWaves * xs_elems(gu_steps);
-  const dim3 g1(a.routes, a.intermediate / kGemvRows);
+  const bool resident = a.shared_gate != nullptr;
+  if (resident && (a.shared_up == nullptr || a.shared_down == nullptr || a.act_shared == nullptr ||
+                   bf16_wave_steps(a.hidden, kGateUpWaves) * kBf16StepK > xs_elems(gu_steps) ||
+                   a.intermediate > xs_elems((a.intermediate + kStepK - 1) / kStepK)))
+    return hipErrorInvalidValue;
+  const int tokens = a.routes / a.top_k;
+  const dim3 g1(a.routes + (resident ? tokens : 0), a.intermediate / kGemvRows);
   if (stage_events) next_launch_events() = stage_events[0];
   hipError_t err = launch_kernel(decode_gate_up_kernel<kGateUpWaves>, g1, dim3(64 * kGateUpWaves), gu_lds, stream,
                                  a, gu_steps);
   if (err != hipSuccess) return err;
   const int d_steps = (a.intermediate + kStepK - 1) / kStepK;
   const size_t d_lds = sizeof(float) * kMaxDecodeRoutes * kGemvRows +
-                       sizeof(uint16_t) * kDownWaves * xs_elems(d_steps);
+                       sizeof(uint16_t) * kDownWaves * xs_elems(d_steps) +
+                       (resident ? sizeof(float) * kMaxDecodeRoutes * kGemvRows : 0);
   if (stage_events) next_launch_events() = stage_events[1];
   return launch_kernel(decode_down_kernel<kDownWaves>, dim3(a.hidden / kGemvRows), dim3(64 * kDownWaves), d_lds,
                        stream, a);

@@ -179,6 +179,12 @@ struct DecodeArgs {
   // * routed_scale) + shared), and health also requires a finite output
   const uint16_t* shared;      // [tokens, hidden] bf16 shared-expert output
   float routed_scale;          // already a bf16 value
+  // the resident bf16 shared expert computed in the same two kernels (null:
+  // none); its intermediate size equals `intermediate`
+  const uint16_t* shared_gate; // [intermediate, hidden] bf16
+  const uint16_t* shared_up;   // [intermediate, hidden] bf16
+  const uint16_t* shared_down; // [hidden, intermediate] bf16
+  uint16_t* act_shared;        // workspace [tokens, intermediate] bf16
 };
 // The decode kernels stage one wave's K range (<= 2048) in LDS: hidden <= 8192
 // (four waves split it), intermediate <= 2048.

@@ -15,9 +15,11 @@ Work is launched only for the experts the routes select.  On one GPU every
 mesh axis has size 1: ``hidden_local`` is the full hidden state, every expert
 is local and both ``psum`` of the reference are the identity.
 
-The shared expert runs as torch bf16 GEMMs on the same GPU (hipBLASLt) at the
-reference's rounding points; the epilogue ``routed * 2.5 + shared`` is fused
-into the library's route-sum kernel (``glm_moe_moe_layer``).
+The shared expert runs inside the two decode kernels for decode shapes
+(``glm_moe_moe_layer_resident``: one pass over HBM for routed and shared
+weights), else as torch bf16 GEMMs on the same GPU (hipBLASLt), at the
+reference's rounding points; the epilogue ``routed * 2.5 + shared`` is always
+fused into the library's route-sum kernel.
 """
 
 from __future__ import annotations
@@ -191,6 +193,7 @@ def routed_experts(
     out: torch.Tensor | None = None,
     events: StageEvents | None = None,
     shared: torch.Tensor | None = None,
+    shared_tables: tuple[torch.Tensor, torch.Tensor, torch.Tensor] | None = None,
     routed_scale: float = 2.5,
 ) -> tuple[torch.Tensor, torch.Tensor]:
     """Routed experts of ``[T, H]`` bf16 rows: ``(bf16 [T, H], valid)``.
@@ -208,7 +211,11 @@ def routed_experts(
     With ``shared`` (the shared expert's bf16 ``[T, H]`` output) the layer
     epilogue is fused into the kernel that finishes the route sum:
     ``bf16(bf16(routed * bf16(routed_scale)) + shared)`` (``:125``, ``:303``),
-    and ``valid`` also requires a finite output (``:126``).
+    and ``valid`` also requires a finite output (``:126``).  ``shared_tables``
+    (its resident bf16 gate, up, down tables) instead computes the shared
+    expert inside the same two decode kernels (decode shapes only:
+    ``uses_decode_kernels``); it streams the shared weights once per row, so
+    the layer bodies use it for a single row.
     """
     if hidden.ndim != 2 or hidden.dtype != torch.bfloat16:
         raise ValueError("routed experts take bf16 [tokens, hidden] rows")
@@ -237,8 +244,21 @@ def routed_experts(
             raise ValueError("shared expert rows must be contiguous bf16 [tokens, hidden]")
         if events is not None:
             raise ValueError("stage events time the routed experts alone")
+    if shared_tables is not None:
+        if shared is not None:
+            raise ValueError("pass the shared expert's output or its tables, not both")
+        if events is not None:
+            raise ValueError("stage events time the routed experts alone")
+        if (
+            len(shared_tables) != 3
+            or any(t.dtype != torch.bfloat16 or not t.is_contiguous() for t in shared_tables)
+            or tuple(shared_tables[0].shape) != (inter, h)
+            or tuple(shared_tables[1].shape) != (inter, h)
+            or tuple(shared_tables[2].shape) != (h, inter)
+        ):
+            raise ValueError("resident shared expert tables must be contiguous bf16 [I, H], [I, H], [H, I]")
     _lib.require_device(hidden, route_indices, route_weights, gate_bits, gate_scale, up_bits, up_scale,
-                        down_bits, down_scale, out, shared)
+                        down_bits, down_scale, out, shared, *(shared_tables or ()))
     device = hidden.device
     if out is None:
         out = torch.empty((tokens, h), dtype=torch.bfloat16, device=device)
@@ -260,7 +280,10 @@ def routed_experts(
         _lib.ptr(gate_bits), _lib.ptr(gate_scale), _lib.ptr(up_bits), _lib.ptr(up_scale), _lib.ptr(down_bits),
         _lib.ptr(down_scale), flags, _lib.ptr(out), _lib.ptr(valid), _lib.ptr(ws), ws.numel(),
     ]
-    if shared is not None:
+    if shared_tables is not None:
+        args[15:15] = [*(_lib.ptr(t) for t in shared_tables), inter, float(routed_scale)]
+        _lib.call("glm_moe_moe_layer_resident", *args, _lib.stream_of(hidden))
+    elif shared is not None:
         args[15:15] = [_lib.ptr(shared), float(routed_scale)]
         _lib.call("glm_moe_moe_layer", *args, _lib.stream_of(hidden))
     elif events is None:
@@ -269,6 +292,12 @@ def routed_experts(
         _lib.call("glm_moe_routed_experts_timed", *args, events.array, ctypes.byref(events.timed),
                   _lib.stream_of(hidden))
     return out, valid
+
+
+def uses_decode_kernels(tokens: int, top_k: int, hidden: int, intermediate: int) -> bool:
+    """Whether a layer of this geometry runs on the two decode kernels (where the
+    shared expert can run inside them)."""
+    return bool(_lib.lib().glm_moe_uses_decode_kernels(tokens, top_k, hidden, intermediate))
 
 
 def _shared_swiglu(hidden: torch.Tensor, gate: torch.Tensor, up: torch.Tensor, down: torch.Tensor) -> torch.Tensor:
@@ -342,11 +371,17 @@ def prefill_moe_from_routes(
         or tuple(shared_down_local.shape) != (h, inter)
     ):
         raise ValueError("prefill shared expert geometry differs from contract")
-    shared = _shared_swiglu(hidden_local, shared_gate_local, shared_up_local, shared_down_local)
+    tables = (shared_gate_local, shared_up_local, shared_down_local)
+    if hidden_local.shape[0] == 1 and uses_decode_kernels(1, contract.top_k, h, inter):
+        # one row: the shared expert runs inside the two decode kernels (with more
+        # rows they would stream its weights once per row; hipBLASLt reads them once)
+        shared_kw = {"shared_tables": tuple(t.contiguous() for t in tables)}
+    else:
+        shared_kw = {"shared": _shared_swiglu(hidden_local, *tables)}
     return routed_experts(
         hidden_local, route_indices, route_weights, expert_gate_bits_local, expert_gate_scale_local,
         expert_up_bits_local, expert_up_scale_local, expert_down_bits_local, expert_down_scale_local,
-        route_sum="float32", check_weights=True, shared=shared, routed_scale=contract.routed_scaling_factor,
+        route_sum="float32", check_weights=True, routed_scale=contract.routed_scaling_factor, **shared_kw,
     )
 
 
@@ -387,11 +422,14 @@ def moe_grouped_routes(
         or tuple(shared_bf16[2].shape) != (h, inter)
     ):
         raise ValueError("grouped MoE BF16 shared tables drifted")
-    shared = _shared_swiglu(hidden_local, *shared_bf16)
+    if uses_decode_kernels(1, contract.top_k, h, inter):
+        shared_kw = {"shared_tables": tuple(t.contiguous() for t in shared_bf16)}
+    else:
+        shared_kw = {"shared": _shared_swiglu(hidden_local, *shared_bf16)}
     output, _ = routed_experts(
         hidden_local, route_indices, route_weights, expert_gate_bits_local, expert_gate_scale_local,
         expert_up_bits_local, expert_up_scale_local, expert_down_bits_local, expert_down_scale_local,
-        route_sum="bfloat16", check_weights=False, drop_unowned=True, shared=shared,
-        routed_scale=contract.routed_scaling_factor,
+        route_sum="bfloat16", check_weights=False, drop_unowned=True,
+        routed_scale=contract.routed_scaling_factor, **shared_kw,
     )
     return output

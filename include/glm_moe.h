@@ -200,6 +200,33 @@ int glm_moe_moe_layer(const uint16_t* hidden, int64_t tokens, int64_t hidden_siz
                       const uint16_t* shared, float routed_scale, uint16_t* out, uint8_t* valid,
                       void* workspace, size_t workspace_bytes, void* stream);
 
+/* 1 when a layer of this geometry runs on the decode kernels (tokens * top_k
+ * <= 64 and the hidden / intermediate sizes they stage), the shapes
+ * glm_moe_moe_layer_resident takes; else 0.  Host-only query, no reference
+ * counterpart (the reference picks its layer body by program, not by shape). */
+int glm_moe_uses_decode_kernels(int64_t tokens, int32_t top_k, int64_t hidden_size, int64_t intermediate);
+
+/* The whole decode MoE layer in two kernels: glm_moe_moe_layer with the
+ * shared expert computed inside the same launches from its resident bf16
+ * tables (gate/up [shared_intermediate, hidden_size], down [hidden_size,
+ * shared_intermediate]; shared_intermediate must equal intermediate) instead
+ * of a caller-computed output -- one pass over HBM for routed and shared
+ * weights.  Replaces moe_grouped_routes' shared expert and epilogue
+ * (glm_tpu/layers/moe/routed_experts.py:269-304; resident_matmul,
+ * glm_tpu/layers/linear.py:26-33): bf16 operands, FP32 sums, bf16 rounding of
+ * gate/up, SwiGLU and down.  Decode shapes only (tokens * top_k <= 64); the
+ * shared weights are streamed once per token, so it pays for a single row (the
+ * decode body).  Same workspace as glm_moe_routed_experts. */
+int glm_moe_moe_layer_resident(const uint16_t* hidden, int64_t tokens, int64_t hidden_size,
+                               const int32_t* route_indices, const float* route_weights, int32_t top_k,
+                               int32_t num_experts, int64_t intermediate, const uint8_t* gate_bits,
+                               const float* gate_scale, const uint8_t* up_bits, const float* up_scale,
+                               const uint8_t* down_bits, const float* down_scale, uint32_t flags,
+                               const uint16_t* shared_gate, const uint16_t* shared_up,
+                               const uint16_t* shared_down, int64_t shared_intermediate, float routed_scale,
+                               uint16_t* out, uint8_t* valid, void* workspace, size_t workspace_bytes,
+                               void* stream);
+
 /* Synthetic FP8 expert tables for tests and benchmarks, the reference's fixture
  * recipe (tools/equivalence/fixture.py:158-172) with 128x128 block scales:
  * w ~ N(0, sigma) (counter-based hash + Box-Muller), scale = amax/448 per block,

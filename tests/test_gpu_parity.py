@@ -374,6 +374,60 @@ def test_fused_layer_nonfinite_output_clears_health(device, tokens, top_k):
     assert bool(ok)  # health is recomputed on every call
 
 
+# ----------------------------------------------------------------------------- resident shared expert
+# glm_moe_moe_layer_resident: the bf16 shared expert inside the two decode
+# kernels; the whole layer against the oracle's moe_layer (routed_experts.py:
+# 119-127 / 269-304) and against the hipBLASLt shared expert + fused epilogue.
+@pytest.mark.parametrize("tokens,experts,hidden,inter,top_k,decode", [
+    (1, 16, 512, 256, 8, True),     # the decode body: bf16 route sum
+    (3, 16, 512, 256, 4, False),    # the prefill body on few rows: FP32 sum
+    (8, 32, 768, 384, 8, False),    # 64 routes, the decode kernels' limit
+    (2, 8, 6144, 2048, 4, True),    # production hidden / intermediate sizes
+])
+def test_resident_shared_expert_layer(device, tokens, experts, hidden, inter, top_k, decode):
+    from glm_moe.layers.moe.routed_experts import _shared_swiglu, routed_experts, uses_decode_kernels
+
+    assert uses_decode_kernels(tokens, top_k, hidden, inter)
+    cfg, x, ids, w, tables = _small_case(tokens, experts, hidden, inter, top_k, 0.0, seed=tokens + 90)
+    t = _device_tables(tables, device)
+    rng = np.random.default_rng(tokens)
+    # weights scaled so that the shared output is O(1) at every size (the absolute
+    # max-abs bound is meaningful only against outputs of that magnitude)
+    shared_f32 = [(rng.standard_normal(shape) * std).astype(np.float32)
+                  for shape, std in (((inter, hidden), hidden ** -0.5), ((inter, hidden), hidden ** -0.5),
+                                     ((hidden, inter), 2 * inter ** -0.5))]
+    shared_dev = [bf16_dev(a, device) for a in shared_f32]
+    kw = dict(route_sum="bfloat16", check_weights=False, drop_unowned=True) if decode else {}
+    args = (bf16_dev(x, device), dev(ids, device), dev(w, device), *(t[k] for k in TABLE_KEYS))
+    got, ok = routed_experts(*args, shared_tables=tuple(shared_dev), **kw)
+    ref, ref_ok = O.moe_layer(x, ids, w, **tables, shared_gate=shared_f32[0], shared_up=shared_f32[1],
+                              shared_down=shared_f32[2], decode=decode)
+    assert bool(ok) == ref_ok
+    print(cfg, "vs oracle:", assert_moe_close(host_f32(got), ref))
+    # the same layer with the shared expert on hipBLASLt: equal up to FP32 summation order
+    shared = _shared_swiglu(args[0], *shared_dev)
+    other, _ = routed_experts(*args, shared=shared, **kw)
+    print("vs hipBLASLt shared expert:", assert_moe_close(host_f32(got), host_f32(other)))
+    again, _ = routed_experts(*args, shared_tables=tuple(shared_dev), **kw)
+    np.testing.assert_array_equal(bf16_bits_of(again), bf16_bits_of(got))  # deterministic
+
+
+def test_resident_shared_expert_nonfinite_clears_health(device):
+    from glm_moe.layers.moe.routed_experts import routed_experts
+
+    cfg, x, ids, w, tables = _small_case(2, 16, 512, 256, 4, 0.0, seed=5)
+    t = _device_tables(tables, device)
+    args = (bf16_dev(x, device), dev(ids, device), dev(w, device), *(t[k] for k in TABLE_KEYS))
+    shared = [torch.zeros(s, dtype=torch.bfloat16, device=device) for s in ((256, 512), (256, 512), (512, 256))]
+    _, ok = routed_experts(*args, shared_tables=tuple(shared))
+    assert bool(ok)
+    shared[2][17, 3] = float("inf")   # shared down row 17: one output column of every token
+    shared[0][3, :] = 1.0             # a non-zero activation in intermediate row 3
+    shared[1][3, :] = 1.0
+    out, ok = routed_experts(*args, shared_tables=tuple(shared))
+    assert not bool(ok) and not bool(torch.isfinite(out[:, 17].float()).all())
+
+
 def _small_case(tokens, experts, hidden, inter, top_k, zipf, seed):
     from glm_moe import synthetic as S
 

@@ -106,6 +106,20 @@ def test_static_refusals_raise_value_error_through_the_abi():
                                    fake, ctypes.c_float(float("inf")), fake, fake, fake, 1 << 30, null)
     with pytest.raises(ValueError, match="routed scale must be finite"):
         _lib.check(status)
+    # the resident shared expert runs on decode shapes only, and needs I_shared == I
+    status = lib.glm_moe_moe_layer_resident(fake, 300, 6144, fake, fake, 8, 256, 2048, fake, fake, fake, fake, fake,
+                                            fake, 0, fake, fake, fake, 2048, ctypes.c_float(2.5), fake, fake, fake,
+                                            1 << 30, null)
+    with pytest.raises(ValueError, match="decode shapes"):
+        _lib.check(status)
+    status = lib.glm_moe_moe_layer_resident(fake, 1, 6144, fake, fake, 8, 256, 2048, fake, fake, fake, fake, fake,
+                                            fake, 0, fake, fake, fake, 1024, ctypes.c_float(2.5), fake, fake, fake,
+                                            1 << 30, null)
+    with pytest.raises(ValueError, match="intermediate size"):
+        _lib.check(status)
+    assert lib.glm_moe_uses_decode_kernels(1, 8, 6144, 2048) == 1
+    assert lib.glm_moe_uses_decode_kernels(9, 8, 6144, 2048) == 0
+    assert lib.glm_moe_uses_decode_kernels(8, 8, 6144, 4096) == 0
 
 
 def test_python_api_refuses_bad_geometry_and_cpu_tensors():
