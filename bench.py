@@ -131,8 +131,44 @@ def run_steps(work, steps, warmup, with_stage_events=True):
     return ms, stages, order
 
 
+def run_steps_graph(work, steps, warmup):
+    """Time `steps` layer calls replayed from one HIP graph (ms per step): the
+    calls, cycling through the rotated routings, are captured once after eager
+    warmup and the graph is replayed between two synchronisations, so the time
+    is the GPU's, without the host's per-call launch cost (a serving loop
+    replays decode steps the same way)."""
+    import torch
+
+    from glm_moe.layers.moe.routed_experts import routed_experts
+
+    t = work.tables
+    tables = [t[k] for k in TABLE_KEYS]
+    out = torch.empty((work.cfg.tokens, work.cfg.hidden), dtype=torch.bfloat16, device=tables[0].device)
+    n_rot = len(work.inputs)
+    for i in range(max(warmup, 1)):
+        x, ids, w = work.inputs[i % n_rot]
+        routed_experts(x, ids, w, *tables, out=out, activations=work.activations)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for i in range(steps):
+            x, ids, w = work.inputs[(warmup + i) % n_rot]
+            routed_experts(x, ids, w, *tables, out=out, activations=work.activations)
+    graph.replay()  # warm replay
+    start = torch.cuda.Event(enable_timing=True)
+    stop = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record()
+    graph.replay()
+    stop.record()
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(stop) / steps
+    del graph
+    return ms
+
+
 def full_layer(work, steps, warmup):
-    """The whole MoE layer, as the reference's layer bodies compute it: the bf16
+    """The whole MoE layer (K calls replayed from one HIP graph), as the reference's layer bodies compute it: the bf16
     shared expert (random-init N(0, 0.02) weights of the contract's shape,
     I_shared = I) and the routed experts with the epilogue
     bf16(bf16(routed * 2.5) + shared) fused into their route-sum kernel.  On
@@ -169,16 +205,22 @@ def full_layer(work, steps, warmup):
             routed_experts(x, ids, w, *tables, out=out, shared=shared, routed_scale=2.5,
                            activations=work.activations)
 
-    for i in range(warmup):
+    for i in range(max(warmup, 1)):
         layer(i)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for i in range(steps):
+            layer(warmup + i)
+    graph.replay()
     start = torch.cuda.Event(enable_timing=True)
     stop = torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     start.record()
-    for i in range(steps):
-        layer(warmup + i)
+    graph.replay()
     stop.record()
     torch.cuda.synchronize()
+    del graph
     shared_bytes = 3 * inter_shared * cfg.hidden * 2
     how = ("shared expert inside the two decode kernels (glm_moe_moe_layer_resident)" if resident else
            "shared expert on torch/hipBLASLt, epilogue fused (glm_moe_moe_layer)")
@@ -345,11 +387,14 @@ def main():
     torch.cuda.synchronize()
     work = Workload(cfg, tables, device)
     print(f"[bench] timing {args.steps} steps after {args.warmup} warmups", file=sys.stderr, flush=True)
-    # headline: a clean loop (no events between the kernels); per-kernel times: a
-    # second loop with HIP events recorded on the launch stream around every stage
-    ms, _, _ = run_steps(work, args.steps, args.warmup, with_stage_events=False)
+    # headline: the K steps replayed from one HIP graph (the eager loop beside it);
+    # per-kernel times: an eager loop with HIP events the kernels record on the
+    # launch stream around every stage
+    ms_eager, _, _ = run_steps(work, args.steps, args.warmup, with_stage_events=False)
+    ms = run_steps_graph(work, args.steps, args.warmup)
     ms_ev, stages, order = run_steps(work, args.steps, args.warmup)
     head = summarize(work, ms, stages, order)
+    head["us_per_layer_eager"] = ms_eager * 1e3
     head["us_per_layer_with_stage_events"] = ms_ev * 1e3
 
     with_full_layer(head, work, args.steps)
@@ -366,9 +411,11 @@ def main():
         activations = "float8_e4m3fn" if mode == "fp8" else "bfloat16"
         print(f"[bench] secondary {name}", file=sys.stderr, flush=True)
         swork = Workload(scfg, tables, device, rotations=8, activations=activations)
-        sms, _, _ = run_steps(swork, args.secondary_steps, 3, with_stage_events=False)
+        sms_eager, _, _ = run_steps(swork, args.secondary_steps, 3, with_stage_events=False)
+        sms = run_steps_graph(swork, args.secondary_steps, 3)
         _, sstages, sorder = run_steps(swork, args.secondary_steps, 3)
         s = summarize(swork, sms, sstages, sorder)
+        s["us_per_layer_eager"] = sms_eager * 1e3
         s["hbm_frac"] = s["layer_hbm_gbs"] / HBM_PEAK_GBS
         s["bf16_mfma_frac"] = s["layer_tflops"] / BF16_PEAK_TFLOPS
         with_full_layer(s, swork, args.secondary_steps)
@@ -411,7 +458,10 @@ def main():
         "layer_hbm_gbs": head["layer_hbm_gbs"],
         "layer_hbm_frac": head["layer_hbm_gbs"] / HBM_PEAK_GBS,
         "stage_us": head["stage_us"],
+        "us_per_layer_eager": head["us_per_layer_eager"],
         "us_per_layer_with_stage_events": head["us_per_layer_with_stage_events"],
+        "timing": "value: K layer calls replayed from one HIP graph between two synchronisations; "
+                  "us_per_layer_eager: the same K calls launched one by one from Python",
         "distinct_experts": head["distinct_experts"],
         "roofline": roofline,
         "cpu_baseline": baseline,

@@ -478,7 +478,9 @@ void decode_gate_up_kernel(const DecodeArgs a, int wave_steps) {
 }
 
 // ------------------------------------------------------------------ down + weighting + combine
-template <int WAVES>
+// RESIDENT: the resident shared expert's down rows are computed here too (a
+// separate instantiation, so the routed-only kernel keeps its registers).
+template <int WAVES, bool RESIDENT>
 __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(4)))
 void decode_down_kernel(const DecodeArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
@@ -497,10 +499,10 @@ void decode_down_kernel(const DecodeArgs a) {
   float(*res_sh)[kGemvRows] = reinterpret_cast<float(*)[kGemvRows]>(
       smem + sizeof(float) * kMaxDecodeRoutes * kGemvRows + sizeof(uint16_t) * WAVES * xs_elems(steps));
   const int tokens = a.routes / a.top_k;
-  const int active = decode_active_routes(a.ids, a.routes, a.experts, a.drop_unowned);
-  const int jobs = active + (a.shared_gate != nullptr ? tokens : 0);
+  const int active = RESIDENT ? decode_active_routes(a.ids, a.routes, a.experts, a.drop_unowned) : kMaxDecodeRoutes;
+  const int jobs = RESIDENT ? active + tokens : kMaxDecodeRoutes;
   for (int j = wave; j < jobs; j += WAVES) {
-    if (j >= active) {
+    if (RESIDENT && j >= active) {
       // the resident shared expert's down projection of token j - active (bf16, unweighted)
       const int t = j - active;
       Bf16Stream<1> g;
@@ -557,7 +559,7 @@ void decode_down_kernel(const DecodeArgs a) {
       if (a.bf16_sum) sum = round_to_bf16(sum);
     }
     const int64_t o = (int64_t)t * H + row0 + row;
-    if (a.shared_gate != nullptr) {
+    if (RESIDENT) {
       // layer epilogue with the resident shared expert computed above
       sum = round_to_bf16(round_to_bf16(round_to_bf16(sum) * a.routed_scale) + res_sh[t][row]);
       if (!isfinite(sum)) a.valid[0] = 0;
@@ -622,8 +624,11 @@ hipError_t launch_decode_routed(const DecodeArgs& a, hipStream_t stream, const L
                        sizeof(uint16_t) * kDownWaves * xs_elems(d_steps) +
                        (resident ? sizeof(float) * kMaxDecodeRoutes * kGemvRows : 0);
   if (stage_events) next_launch_events() = stage_events[1];
-  return launch_kernel(decode_down_kernel<kDownWaves>, dim3(a.hidden / kGemvRows), dim3(64 * kDownWaves), d_lds,
-                       stream, a);
+  if (resident)
+    return launch_kernel(decode_down_kernel<kDownWaves, true>, dim3(a.hidden / kGemvRows), dim3(64 * kDownWaves),
+                         d_lds, stream, a);
+  return launch_kernel(decode_down_kernel<kDownWaves, false>, dim3(a.hidden / kGemvRows), dim3(64 * kDownWaves),
+                       d_lds, stream, a);
 }
 
 }  // namespace glm_moe

@@ -1,0 +1,60 @@
+"""Layer calls captured in a HIP graph (torch.cuda.CUDAGraph) replay to the same
+bits as eager calls, replay after replay, with eager work between replays."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+
+
+TABLE_KEYS = ("gate_bits", "gate_scale", "up_bits", "up_scale", "down_bits", "down_scale")
+
+
+def _case(tokens, experts, hidden, inter, top_k, seed):
+    from glm_moe import synthetic as S
+
+    cfg = S.MoeConfig("graph", tokens, experts, hidden, inter, top_k, 0.0)
+    x = torch.from_numpy(S.hidden_states(cfg, seed)).to(torch.bfloat16).cuda()
+    ids, w = (torch.from_numpy(a).cuda() for a in S.routes(cfg, seed))
+    t = S.host_expert_tables(cfg, seed)
+    return x, ids, w, [torch.from_numpy(t[k]).cuda() for k in TABLE_KEYS]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("tokens,experts,hidden,inter,top_k,mode", [
+    (1, 16, 512, 256, 8, "routed"),     # decode kernels
+    (1, 16, 512, 256, 8, "resident"),   # decode kernels with the resident shared expert
+    (300, 64, 256, 512, 6, "shared"),   # route plan + grouped GEMMs + combine with the fused epilogue
+    (512, 16, 512, 256, 8, "routed"),   # prefill kernels
+])
+def test_graph_replays_match_eager(tokens, experts, hidden, inter, top_k, mode):
+    from glm_moe.layers.moe.routed_experts import routed_experts
+
+    x, ids, w, tables = _case(tokens, experts, hidden, inter, top_k, seed=tokens + 7)
+    x2, ids2, w2, _ = _case(tokens, experts, hidden, inter, top_k, seed=tokens + 8)
+    kw = {}
+    if mode == "resident":
+        g = torch.Generator(device="cuda").manual_seed(1)
+        kw["shared_tables"] = tuple((torch.randn(s, generator=g, device="cuda") * 0.05).to(torch.bfloat16)
+                                    for s in ((inter, hidden), (inter, hidden), (hidden, inter)))
+    elif mode == "shared":
+        kw["shared"] = (torch.randn((tokens, hidden), device="cuda") * 0.1).to(torch.bfloat16)
+    out = torch.empty((tokens, hidden), dtype=torch.bfloat16, device="cuda")
+    eager, ok = routed_experts(x, ids, w, *tables, out=out, **kw)
+    eager = eager.clone()
+    other, _ = routed_experts(x2, ids2, w2, *tables, **kw)  # a different eager result
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        _, valid = routed_experts(x, ids, w, *tables, out=out, **kw)
+    for replay in range(3):
+        out.zero_()
+        routed_experts(x2, ids2, w2, *tables, out=out, **kw)  # eager work into the same buffers
+        torch.cuda.synchronize()
+        assert torch.equal(out, other)
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), f"replay {replay} differs from the eager result"
+        assert bool(valid) == bool(ok)
