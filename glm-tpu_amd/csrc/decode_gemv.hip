@@ -2,7 +2,7 @@
 // top-8): two kernels, no separate route plan and no separate combine.
 //
 // 1. gate/up: workgroup = (route j, 16 intermediate rows); WK waves split K.
-// 2. down:    workgroup = 16 hidden rows x every route; its waves take routes
+// 2. down:    workgroup = 8 hidden rows x every route; its waves take routes
 //    in turn, write each route's weighted bf16 result to LDS, and the
 //    workgroup then sums every token's slots in slot order (the route combine
 //    of glm_tpu/layers/moe/routed_experts.py:104-117 / :291-293).
@@ -12,7 +12,7 @@
 // outside [0, experts) are skipped (drop_unowned) or use expert 0, the
 // reference's safe id.
 //
-// Projections are GEMVs on the vector ALU.  A wave owns 16 weight rows and a
+// Projections are GEMVs on the vector ALU.  A wave owns 16 (gate/up) or 8 (down) weight rows and a
 // range of K "steps" of 256.  Each 128-bit load instruction covers 4 rows x
 // 256 contiguous bytes (lane l: row 4q + l/16, bytes (l%16)*16), the access
 // pattern that streams HBM at full rate; weight loads are the only vector
@@ -43,7 +43,9 @@ constexpr int kMaxWaveSteps = 8;   // K range of one wave: 2048 (LDS staging, la
 constexpr int kGateUpWaves = 4;
 constexpr int kDownWaves = 8;
 constexpr int kGateUpDepth = 2;    // two tables: 2 x 32 VGPRs in flight
-constexpr int kDownDepth = 3;      // one table: 3 x 16 VGPRs in flight
+constexpr int kDownRows = 8;       // down: weight rows per workgroup (H / 8 = 768 workgroups: 3 per CU)
+constexpr int kDownQuads = kDownRows / 4;
+constexpr int kDownDepth = 6;      // one table, 8 rows: 6 x 8 VGPRs in flight
 
 constexpr int kNonTemporal = 2;            // buffer load cache policy: streamed once (nt)
 constexpr int kBufferFormat = 0x00020000;  // raw buffer descriptor word 3: 32-bit data format
@@ -138,8 +140,8 @@ __device__ __forceinline__ void stage_x_store(const GemvStream<TABLES>& g, int l
 // FULL: every step of the range is whole.  Otherwise the masked lanes of a
 // half step (the last step of an odd k/128) load the row's last 16 bytes, in
 // bounds; their products are zero.
-template <bool FULL, int TABLES>
-__device__ __forceinline__ void gemv_load(const GemvStream<TABLES>& g, int s, int lane, u32x4 (&w)[TABLES][4]) {
+template <bool FULL, int TABLES, int QN>
+__device__ __forceinline__ void gemv_load(const GemvStream<TABLES>& g, int s, int lane, u32x4 (&w)[TABLES][QN]) {
   // buffer loads: lane offset (VGPR) + step (immediate) + row group and range start (SGPR)
   uint32_t off = g.lane_off + s * kStepK;
   if constexpr (!FULL) {
@@ -149,16 +151,16 @@ __device__ __forceinline__ void gemv_load(const GemvStream<TABLES>& g, int s, in
 #pragma unroll
   for (int t = 0; t < TABLES; ++t)
 #pragma unroll
-    for (int q = 0; q < 4; ++q)
+    for (int q = 0; q < QN; ++q)
       w[t][q] = __builtin_bit_cast(
           u32x4, __builtin_amdgcn_raw_buffer_load_b128(g.w[t], off, 4 * q * (int)g.row_stride + g.step_begin * kStepK,
                                                        kNonTemporal));
 }
 
 // acc[t][q] += sum over the lane's 16 K of bf16(e4m3 * scale) * x, for step s0 + s
-template <bool FULL, int TABLES>
-__device__ __forceinline__ void gemv_fma(const GemvStream<TABLES>& g, const u32x4 (&w)[TABLES][4], int s,
-                                         int lane, float (&acc)[TABLES][4]) {
+template <bool FULL, int TABLES, int QN>
+__device__ __forceinline__ void gemv_fma(const GemvStream<TABLES>& g, const u32x4 (&w)[TABLES][QN], int s,
+                                         int lane, float (&acc)[TABLES][QN]) {
   int xoff = s * kStepK + (lane & 15) * 16;
   int b_hi = 2 * s + 1;
   bool keep = true;
@@ -176,7 +178,7 @@ __device__ __forceinline__ void gemv_fma(const GemvStream<TABLES>& g, const u32x
     float scale = (lane & 15) < 8 ? s_lo : s_hi;
     if constexpr (!FULL) scale = keep ? scale : 0.0f;
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
+    for (int q = 0; q < QN; ++q) {
       const u32x4 lo = __builtin_bit_cast(u32x4, decode_fp8x8(w[t][q][0], w[t][q][1], scale));
       const u32x4 hi = __builtin_bit_cast(u32x4, decode_fp8x8(w[t][q][2], w[t][q][3], scale));
       float a = acc[t][q];
@@ -200,13 +202,13 @@ __device__ __forceinline__ void gemv_fma(const GemvStream<TABLES>& g, const u32x
 // the step it is about to multiply.  Order of issue: activation staging
 // loads, the first DEPTH weight steps, then the staging stores (which wait
 // for the activations only).
-template <int NSTEPS, int DEPTH, int TABLES>
-__device__ __forceinline__ void gemv_run_fixed(const GemvStream<TABLES>& g, int lane, float (&acc)[TABLES][4]) {
+template <int NSTEPS, int DEPTH, int TABLES, int QN>
+__device__ __forceinline__ void gemv_run_fixed(const GemvStream<TABLES>& g, int lane, float (&acc)[TABLES][QN]) {
   constexpr int D = DEPTH < NSTEPS ? DEPTH : NSTEPS;
   u32x4 xv[4];
   stage_x_load(g, lane, xv);
   __builtin_amdgcn_sched_barrier(0);
-  u32x4 ring[D][TABLES][4];
+  u32x4 ring[D][TABLES][QN];
 #pragma unroll
   for (int d = 0; d < D; ++d) {
     gemv_load<true>(g, d, lane, ring[d]);
@@ -227,13 +229,13 @@ __device__ __forceinline__ void gemv_run_fixed(const GemvStream<TABLES>& g, int 
 
 // Any range, half step included: a loop over groups of DEPTH steps whose
 // refills are issued unconditionally (a refill past the end reloads the last step).
-template <int DEPTH, int TABLES>
-__device__ __forceinline__ void gemv_run_loop(const GemvStream<TABLES>& g, int lane, float (&acc)[TABLES][4]) {
+template <int DEPTH, int TABLES, int QN>
+__device__ __forceinline__ void gemv_run_loop(const GemvStream<TABLES>& g, int lane, float (&acc)[TABLES][QN]) {
   const int n = g.step_end - g.step_begin, last = n - 1;
   u32x4 xv[4];
   stage_x_load(g, lane, xv);
   __builtin_amdgcn_sched_barrier(0);
-  u32x4 ring[DEPTH][TABLES][4];
+  u32x4 ring[DEPTH][TABLES][QN];
 #pragma unroll
   for (int d = 0; d < DEPTH; ++d) {
     gemv_load<false>(g, min(d, last), lane, ring[d]);
@@ -252,8 +254,8 @@ __device__ __forceinline__ void gemv_run_loop(const GemvStream<TABLES>& g, int l
   }
 }
 
-template <int DEPTH, int TABLES>
-__device__ __forceinline__ void gemv_run(const GemvStream<TABLES>& g, int lane, float (&acc)[TABLES][4]) {
+template <int DEPTH, int TABLES, int QN>
+__device__ __forceinline__ void gemv_run(const GemvStream<TABLES>& g, int lane, float (&acc)[TABLES][QN]) {
   const int n = g.step_end - g.step_begin;
   if (n <= 0) return;
   // a half step exists when k / 128 is odd; it is the last step of the last range
@@ -311,26 +313,26 @@ struct Bf16Stream {
   uint16_t* xs;        // the wave's LDS region (the K range)
 };
 
-template <int TABLES>
-__device__ __forceinline__ void bf16_load(const Bf16Stream<TABLES>& g, int s, u32x4 (&w)[TABLES][4]) {
+template <int TABLES, int QN>
+__device__ __forceinline__ void bf16_load(const Bf16Stream<TABLES>& g, int s, u32x4 (&w)[TABLES][QN]) {
   const uint32_t off = g.lane_off + s * kStepK;
 #pragma unroll
   for (int t = 0; t < TABLES; ++t)
 #pragma unroll
-    for (int q = 0; q < 4; ++q)
+    for (int q = 0; q < QN; ++q)
       w[t][q] = __builtin_bit_cast(
           u32x4, __builtin_amdgcn_raw_buffer_load_b128(g.w[t], off, 4 * q * g.row_bytes + g.step_begin * kStepK,
                                                        kNonTemporal));
 }
 
-template <int TABLES>
-__device__ __forceinline__ void bf16_fma(const Bf16Stream<TABLES>& g, const u32x4 (&w)[TABLES][4], int s, int lane,
-                                         float (&acc)[TABLES][4]) {
+template <int TABLES, int QN>
+__device__ __forceinline__ void bf16_fma(const Bf16Stream<TABLES>& g, const u32x4 (&w)[TABLES][QN], int s, int lane,
+                                         float (&acc)[TABLES][QN]) {
   const u32x4 x = *reinterpret_cast<const u32x4*>(g.xs + s * kBf16StepK + (lane & 15) * 8);
 #pragma unroll
   for (int t = 0; t < TABLES; ++t)
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
+    for (int q = 0; q < QN; ++q) {
       float a = acc[t][q];
 #pragma unroll
       for (int h = 0; h < 4; ++h) {
@@ -343,8 +345,8 @@ __device__ __forceinline__ void bf16_fma(const Bf16Stream<TABLES>& g, const u32x
 
 // The wave's K range with DEPTH steps of weights in flight; the activations
 // are staged once into the wave's LDS region (loads issued before the weights).
-template <int DEPTH, int TABLES>
-__device__ __forceinline__ void bf16_run(const Bf16Stream<TABLES>& g, int lane, float (&acc)[TABLES][4]) {
+template <int DEPTH, int TABLES, int QN>
+__device__ __forceinline__ void bf16_run(const Bf16Stream<TABLES>& g, int lane, float (&acc)[TABLES][QN]) {
   const int n = g.step_end - g.step_begin;
   if (n <= 0) return;
   const int last = n - 1;
@@ -357,7 +359,7 @@ __device__ __forceinline__ void bf16_run(const Bf16Stream<TABLES>& g, int lane, 
     if (c < chunks) xv[i] = *reinterpret_cast<const u32x4*>(g.x + kbeg + 8 * c);
   }
   __builtin_amdgcn_sched_barrier(0);
-  u32x4 ring[DEPTH][TABLES][4];
+  u32x4 ring[DEPTH][TABLES][QN];
 #pragma unroll
   for (int d = 0; d < DEPTH; ++d) {
     bf16_load(g, min(d, last), ring[d]);
@@ -489,7 +491,7 @@ void decode_down_kernel(const DecodeArgs a) {
   const int wave = uniform(threadIdx.x >> 6);  // wave-uniform: scalar loop control
   const int tid = threadIdx.x;
   const int I = a.intermediate, H = a.hidden;
-  const int row0 = blockIdx.x * kGemvRows;
+  const int row0 = blockIdx.x * kDownRows;
   const int steps = (I + kStepK - 1) / kStepK;
   for (int i = tid; i < a.routes * kGemvRows; i += 64 * WAVES) res[i / kGemvRows][i % kGemvRows] = 0.f;
   __syncthreads();
@@ -512,13 +514,13 @@ void decode_down_kernel(const DecodeArgs a) {
       g.step_begin = 0;
       g.step_end = I / kBf16StepK;
       g.w[0] = rows_buffer(reinterpret_cast<const uint8_t*>(a.shared_down + (int64_t)row0 * I),
-                           (int64_t)kGemvRows * 2 * I);
+                           (int64_t)kDownRows * 2 * I);
       g.x = a.act_shared + (int64_t)t * I;
       g.xs = xs;
-      float acc[1][4] = {};
+      float acc[1][kDownQuads] = {};
       bf16_run<kDownDepth>(g, lane, acc);
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
+      for (int q = 0; q < kDownQuads; ++q) {
         const float v = sum16(acc[0][q]);
         if ((lane & 15) == 0) res_sh[t][4 * q + (lane >> 4)] = round_to_bf16(v);
       }
@@ -532,7 +534,7 @@ void decode_down_kernel(const DecodeArgs a) {
     g.row_stride = I;
     g.step_begin = 0;
     g.step_end = steps;
-    g.w[0] = rows_buffer(a.down_bits + ((int64_t)rt.expert * H + row0) * I, (int64_t)kGemvRows * I);
+    g.w[0] = rows_buffer(a.down_bits + ((int64_t)rt.expert * H + row0) * I, (int64_t)kDownRows * I);
     g.lane_off = (uint32_t)((lane >> 4) * I + (lane & 15) * 16);
     const float* srow = a.down_scale + ((int64_t)rt.expert * (H / kScaleBlock) + row0 / kScaleBlock) * g.kblocks;
     g.sreg[0] = lane_scale(srow, g.kblocks, 0, lane);
@@ -540,10 +542,10 @@ void decode_down_kernel(const DecodeArgs a) {
     g.xs = xs;
     g.pad = steps * kStepK;
     const float wr = round_to_bf16(a.weights[rt.route]);  // loaded before the weight stream
-    float acc[1][4] = {};
+    float acc[1][kDownQuads] = {};
     gemv_run<kDownDepth>(g, lane, acc);
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
+    for (int q = 0; q < kDownQuads; ++q) {
       const float v = sum16(acc[0][q]);
       // bf16 down output times the bf16 route weight, rounded (routed_experts.py:104-105)
       if ((lane & 15) == 0) res[rt.route][4 * q + (lane >> 4)] = round_to_bf16(round_to_bf16(v) * wr);
@@ -551,8 +553,8 @@ void decode_down_kernel(const DecodeArgs a) {
   }
   __syncthreads();
   // route combine: every token's slots in slot order, FP32 (or bf16 running) sum
-  for (int i = tid; i < tokens * kGemvRows; i += 64 * WAVES) {
-    const int t = i / kGemvRows, row = i % kGemvRows;
+  for (int i = tid; i < tokens * kDownRows; i += 64 * WAVES) {
+    const int t = i / kDownRows, row = i % kDownRows;
     float sum = 0.f;
     for (int s = 0; s < a.top_k; ++s) {
       sum += res[t * a.top_k + s][row];
@@ -625,9 +627,9 @@ hipError_t launch_decode_routed(const DecodeArgs& a, hipStream_t stream, const L
                        (resident ? sizeof(float) * kMaxDecodeRoutes * kGemvRows : 0);
   if (stage_events) next_launch_events() = stage_events[1];
   if (resident)
-    return launch_kernel(decode_down_kernel<kDownWaves, true>, dim3(a.hidden / kGemvRows), dim3(64 * kDownWaves),
+    return launch_kernel(decode_down_kernel<kDownWaves, true>, dim3(a.hidden / kDownRows), dim3(64 * kDownWaves),
                          d_lds, stream, a);
-  return launch_kernel(decode_down_kernel<kDownWaves, false>, dim3(a.hidden / kGemvRows), dim3(64 * kDownWaves),
+  return launch_kernel(decode_down_kernel<kDownWaves, false>, dim3(a.hidden / kDownRows), dim3(64 * kDownWaves),
                        d_lds, stream, a);
 }
 
