@@ -231,7 +231,12 @@ def full_layer(work, steps, warmup):
 
 
 def with_full_layer(s, work, steps):
-    us, shared_bytes, how = full_layer(work, steps, 3)
+    try:
+        us, shared_bytes, how = full_layer(work, steps, 3)
+    except Exception as exc:  # a secondary figure: report it, keep the headline
+        print(f"[bench] full layer failed: {exc!r}", file=sys.stderr, flush=True)
+        s["full_layer_error"] = repr(exc)
+        return s
     s["full_layer_us"] = us
     s["full_layer_hbm_gbs"] = (s["layer_bytes"] + shared_bytes) / (us * 1e-6) / 1e9
     s["full_layer_note"] = f"routed experts + bf16 shared expert + fused routed*2.5+shared epilogue; {how}"
@@ -370,6 +375,25 @@ def cpu_baseline(work, device):
     }
 
 
+def measure_secondary(scfg, tables, device, activations, mode, steps):
+    """Layer time, stage times, full layer and (FP8 mode) error of one secondary config."""
+    swork = Workload(scfg, tables, device, rotations=8, activations=activations)
+    sms_eager, _, _ = run_steps(swork, steps, 3, with_stage_events=False)
+    sms = run_steps_graph(swork, steps, 3)
+    _, sstages, sorder = run_steps(swork, steps, 3)
+    s = summarize(swork, sms, sstages, sorder)
+    s["us_per_layer_eager"] = sms_eager * 1e3
+    s["hbm_frac"] = s["layer_hbm_gbs"] / HBM_PEAK_GBS
+    s["bf16_mfma_frac"] = s["layer_tflops"] / BF16_PEAK_TFLOPS
+    with_full_layer(s, swork, steps)
+    if mode == "fp8":
+        s["activations"] = "float8_e4m3fn (native FP8 MFMA mode)"
+        s["fp8_mfma_frac"] = s["layer_tflops"] / FP8_PEAK_TFLOPS
+        s["error_vs_reference"] = fp8_error(swork, device)
+    del swork
+    return s
+
+
 def main():
     args = parse_args()
     if args.gpus != 1:
@@ -394,7 +418,12 @@ def main():
     # per-kernel times: an eager loop with HIP events the kernels record on the
     # launch stream around every stage
     ms_eager, _, _ = run_steps(work, args.steps, args.warmup, with_stage_events=False)
-    ms = run_steps_graph(work, args.steps, args.warmup)
+    timing_note = None
+    try:
+        ms = run_steps_graph(work, args.steps, args.warmup)
+    except Exception as exc:  # keep a measurement: the eager loop, labelled as such
+        print(f"[bench] graph replay failed: {exc!r}; reporting the eager loop", file=sys.stderr, flush=True)
+        ms, timing_note = ms_eager, f"eager loop (graph replay failed: {exc!r})"
     ms_ev, stages, order = run_steps(work, args.steps, args.warmup)
     head = summarize(work, ms, stages, order)
     head["us_per_layer_eager"] = ms_eager * 1e3
@@ -413,21 +442,11 @@ def main():
         scfg = S.CONFIGS[base]
         activations = "float8_e4m3fn" if mode == "fp8" else "bfloat16"
         print(f"[bench] secondary {name}", file=sys.stderr, flush=True)
-        swork = Workload(scfg, tables, device, rotations=8, activations=activations)
-        sms_eager, _, _ = run_steps(swork, args.secondary_steps, 3, with_stage_events=False)
-        sms = run_steps_graph(swork, args.secondary_steps, 3)
-        _, sstages, sorder = run_steps(swork, args.secondary_steps, 3)
-        s = summarize(swork, sms, sstages, sorder)
-        s["us_per_layer_eager"] = sms_eager * 1e3
-        s["hbm_frac"] = s["layer_hbm_gbs"] / HBM_PEAK_GBS
-        s["bf16_mfma_frac"] = s["layer_tflops"] / BF16_PEAK_TFLOPS
-        with_full_layer(s, swork, args.secondary_steps)
-        if mode == "fp8":
-            s["activations"] = "float8_e4m3fn (native FP8 MFMA mode)"
-            s["fp8_mfma_frac"] = s["layer_tflops"] / FP8_PEAK_TFLOPS
-            s["error_vs_reference"] = fp8_error(swork, device)
-        secondary[name] = s
-        del swork
+        try:
+            secondary[name] = measure_secondary(scfg, tables, device, activations, mode, args.secondary_steps)
+        except Exception as exc:  # a secondary figure: report it, keep the headline
+            print(f"[bench] secondary {name} failed: {exc!r}", file=sys.stderr, flush=True)
+            secondary[name] = {"error": repr(exc)}
 
     baseline = None
     if not args.no_cpu_baseline:
@@ -463,8 +482,9 @@ def main():
         "stage_us": head["stage_us"],
         "us_per_layer_eager": head["us_per_layer_eager"],
         "us_per_layer_with_stage_events": head["us_per_layer_with_stage_events"],
-        "timing": "value: K layer calls replayed from one HIP graph between two synchronisations, after "
-                  "3 untimed replays of it; us_per_layer_eager: the same K calls launched one by one from Python",
+        "timing": timing_note or ("value: K layer calls replayed from one HIP graph between two "
+                                  "synchronisations, after 3 untimed replays of it; us_per_layer_eager: the same "
+                                  "K calls launched one by one from Python"),
         "distinct_experts": head["distinct_experts"],
         "roofline": roofline,
         "cpu_baseline": baseline,
