@@ -188,6 +188,8 @@ int routed_experts_impl(const uint16_t* hidden, int64_t tokens, int64_t hidden_s
                        prefill_fits(intermediate, hidden_size, 2) && prefill_fits(hidden_size, intermediate, 1)),
               "FP8 activations need a prefill shape: more than 8 routes per expert on average, H a multiple of "
               "256 and I of 128, both at most 8192");
+  GLM_REQUIRE(!fp8 || (prefill_rows_fit(tokens, hidden_size) && prefill_rows_fit(n, intermediate)),
+              "FP8 activations: tokens x hidden and routes x intermediate bf16 must stay below 2 GiB");
   const int bn13 = gemm_shape_bn(shape, 2);
   const int bn2 = gemm_shape_bn(shape, 1);
   GLM_REQUIRE(intermediate % bn13 == 0, "intermediate size must be a multiple of %d", bn13);

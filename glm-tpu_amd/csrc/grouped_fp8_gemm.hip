@@ -284,7 +284,8 @@ hipError_t launch_grouped_gemm(const GroupedGemmArgs& a, int shape, int tables, 
       case kShapeSkinny: return launch_shape<2, 1, 16, 1, 4, 1>(a, epilogue, stream);
       case kShapePanel32: return launch_shape<2, 1, 32, 4, 1, 1>(a, epilogue, stream);
       case kShapeWide:
-        return prefill_fits(a.n, a.k, 2) ? launch_grouped_gemm_prefill(a, 2, epilogue, stream)
+        return prefill_fits(a.n, a.k, 2) && prefill_rows_fit(a.x_rows, a.k)
+                   ? launch_grouped_gemm_prefill(a, 2, epilogue, stream)
                                          : launch_grouped_gemm_wide(a, 2, epilogue, stream);
       default: return hipErrorInvalidValue;
     }
@@ -295,7 +296,8 @@ hipError_t launch_grouped_gemm(const GroupedGemmArgs& a, int shape, int tables, 
       case kShapeSkinny: return launch_shape<1, 1, 16, 2, 2, 1>(a, epilogue, stream);
       case kShapePanel32: return launch_shape<1, 2, 32, 4, 1, 1>(a, epilogue, stream);
       case kShapeWide:
-        return prefill_fits(a.n, a.k, 1) ? launch_grouped_gemm_prefill(a, 1, epilogue, stream)
+        return prefill_fits(a.n, a.k, 1) && prefill_rows_fit(a.x_rows, a.k)
+                   ? launch_grouped_gemm_prefill(a, 1, epilogue, stream)
                                          : launch_grouped_gemm_wide(a, 1, epilogue, stream);
       default: return hipErrorInvalidValue;
     }

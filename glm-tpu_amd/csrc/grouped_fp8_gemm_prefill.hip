@@ -597,10 +597,12 @@ int prefill_bn(int tables) { return tables == 2 ? 8 * 16 : 8 * 32; }
 bool prefill_fits(int64_t n, int64_t k, int tables) {
   return n % prefill_bn(tables) == 0 && k % kScaleBlock == 0 && k / kScaleBlock <= 64;
 }
+// Their activation buffer offsets are 32-bit: rows x K bf16 must stay below 2 GiB.
+bool prefill_rows_fit(int64_t x_rows, int64_t k) { return x_rows > 0 && x_rows * k * 2 <= INT32_MAX; }
 hipError_t launch_grouped_gemm_prefill(const GroupedGemmArgs& a, int tables, int epilogue, hipStream_t stream) {
   if (a.max_tiles <= 0) return hipSuccess;
   if (a.expert_first_tile == nullptr || a.expert_tiles == nullptr) return hipErrorInvalidValue;
-  if (!prefill_fits(a.n, a.k, tables)) return hipErrorInvalidValue;
+  if (!prefill_fits(a.n, a.k, tables) || !prefill_rows_fit(a.x_rows, a.k)) return hipErrorInvalidValue;
   if (a.xq != nullptr) {
     if (a.xscale == nullptr) return hipErrorInvalidValue;
     if (tables == 2 && epilogue == kEpiSwiglu)

@@ -147,6 +147,8 @@ hipError_t launch_grouped_gemm_wide(const GroupedGemmArgs& a, int tables, int ep
 // work order); needs the plan's expert_first_tile / expert_tiles.
 int prefill_bn(int tables);
 bool prefill_fits(int64_t n, int64_t k, int tables);
+// The prefill kernels' 32-bit activation offsets: x_rows x k x 2 bytes below 2 GiB.
+bool prefill_rows_fit(int64_t x_rows, int64_t k);
 hipError_t launch_grouped_gemm_prefill(const GroupedGemmArgs& a, int tables, int epilogue, hipStream_t stream);
 hipError_t launch_grouped_gemm(const GroupedGemmArgs& a, int shape, int tables, int epilogue,
                                hipStream_t stream);
