@@ -169,6 +169,47 @@ def run_steps_graph(work, steps, warmup):
     return ms
 
 
+def router_time(cfg, device, steps=20):
+    """The GPU noaux_tc router on the config's [T, E] FP32 logits (replayed from
+    one HIP graph): us per call and its algorithmic bytes (logits in, ids and
+    weights out)."""
+    import torch
+
+    from glm_moe import synthetic as S
+    from glm_moe.layers.moe.router import route_glm_noaux_tc_logits
+
+    logits = torch.from_numpy(S.router_logits(cfg, 0)).to(device)
+    bias = torch.zeros(cfg.experts, dtype=torch.float32, device=device)
+    for _ in range(3):
+        route_glm_noaux_tc_logits(logits, bias, top_k=cfg.top_k)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for _ in range(steps):
+            route_glm_noaux_tc_logits(logits, bias, top_k=cfg.top_k)
+    for _ in range(GRAPH_WARM_REPLAYS):
+        graph.replay()
+    start = torch.cuda.Event(enable_timing=True)
+    stop = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record()
+    graph.replay()
+    stop.record()
+    torch.cuda.synchronize()
+    us = start.elapsed_time(stop) / steps * 1e3
+    nbytes = cfg.tokens * cfg.experts * 4 + cfg.experts * 4 + cfg.tokens * cfg.top_k * 8
+    return {"us": us, "bytes": nbytes, "hbm_gbs": nbytes / (us * 1e-6) / 1e9}
+
+
+def with_router(s, cfg, device):
+    try:
+        s["router"] = router_time(cfg, device)
+    except Exception as exc:  # a secondary figure: report it, keep the headline
+        print(f"[bench] router timing failed: {exc!r}", file=sys.stderr, flush=True)
+        s["router"] = {"error": repr(exc)}
+    return s
+
+
 def full_layer(work, steps, warmup):
     """The whole MoE layer (K calls replayed from one HIP graph), as the reference's layer bodies compute it: the bf16
     shared expert (random-init N(0, 0.02) weights of the contract's shape,
@@ -386,6 +427,8 @@ def measure_secondary(scfg, tables, device, activations, mode, steps):
     s["hbm_frac"] = s["layer_hbm_gbs"] / HBM_PEAK_GBS
     s["bf16_mfma_frac"] = s["layer_tflops"] / BF16_PEAK_TFLOPS
     with_full_layer(s, swork, steps)
+    if mode != "fp8":
+        with_router(s, scfg, device)
     if mode == "fp8":
         s["activations"] = "float8_e4m3fn (native FP8 MFMA mode)"
         s["fp8_mfma_frac"] = s["layer_tflops"] / FP8_PEAK_TFLOPS
@@ -430,6 +473,7 @@ def main():
     head["us_per_layer_with_stage_events"] = ms_ev * 1e3
 
     with_full_layer(head, work, args.steps)
+    with_router(head, cfg, device)
     roofline = dominant_roofline(cfg, head)
     if args.copy_calibration:
         copy_calibration(device)
@@ -474,9 +518,10 @@ def main():
             "tokens": cfg.tokens, "experts": cfg.experts, "hidden": cfg.hidden,
             "intermediate": cfg.intermediate, "top_k": cfg.top_k,
         },
-        "full_layer_us": head["full_layer_us"],
-        "full_layer_hbm_gbs": head["full_layer_hbm_gbs"],
-        "full_layer_note": head["full_layer_note"],
+        "full_layer_us": head.get("full_layer_us"),
+        "full_layer_hbm_gbs": head.get("full_layer_hbm_gbs"),
+        "full_layer_note": head.get("full_layer_note", head.get("full_layer_error")),
+        "router": head["router"],
         "layer_hbm_gbs": head["layer_hbm_gbs"],
         "layer_hbm_frac": head["layer_hbm_gbs"] / HBM_PEAK_GBS,
         "stage_us": head["stage_us"],

@@ -30,6 +30,7 @@
 // b % 8, and XCD x walks the contiguous range [x * per, (x + 1) * per) of work
 // items, so the tiles that share an expert's weight stripe (hot experts) and
 // the stripes that share a tile's activation rows run together on one XCD.
+#include <atomic>
 #include <type_traits>
 
 #include "gemm_epilogue.h"
@@ -556,17 +557,27 @@ __global__ __launch_bounds__(64 * WAVES, 1) void prefill_gemm_fp8_kernel(const G
   }
 }
 
+// Lets `kernel` use the whole 160 KB of LDS on the current device.  `done` is
+// the caller's per-kernel mask of devices already set (the attribute is
+// per device; setting it twice is harmless, so racing threads are fine).
+inline hipError_t allow_full_lds(const void* kernel, std::atomic<uint64_t>& done) {
+  int dev = 0;
+  hipError_t err = hipGetDevice(&dev);
+  if (err != hipSuccess) return err;
+  const uint64_t bit = dev < 64 ? (1ull << dev) : 0;
+  if (bit != 0 && (done.load(std::memory_order_acquire) & bit)) return hipSuccess;
+  err = hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, kPrefillLds);
+  if (err == hipSuccess) done.fetch_or(bit, std::memory_order_release);
+  return err;
+}
+
 template <int TABLES, int RG, int WAVES, int EPI>
 hipError_t launch_prefill_fp8(const GroupedGemmArgs& a, hipStream_t stream) {
   constexpr int BN = WAVES * RG * 16;
-  static bool attr_set = false;
-  if (!attr_set) {
-    const hipError_t err =
-        hipFuncSetAttribute(reinterpret_cast<const void*>(prefill_gemm_fp8_kernel<TABLES, RG, WAVES, EPI>),
-                            hipFuncAttributeMaxDynamicSharedMemorySize, kPrefillLds);
-    if (err != hipSuccess) return err;
-    attr_set = true;
-  }
+  static std::atomic<uint64_t> lds_set{0};
+  const hipError_t err =
+      allow_full_lds(reinterpret_cast<const void*>(prefill_gemm_fp8_kernel<TABLES, RG, WAVES, EPI>), lds_set);
+  if (err != hipSuccess) return err;
   const int64_t items = (int64_t)(a.n / BN) * a.max_tiles;
   const int64_t grid = (items + kXcds - 1) / kXcds * kXcds;
   return launch_kernel(prefill_gemm_fp8_kernel<TABLES, RG, WAVES, EPI>, dim3((unsigned)grid), dim3(64 * WAVES),
@@ -575,14 +586,10 @@ hipError_t launch_prefill_fp8(const GroupedGemmArgs& a, hipStream_t stream) {
 template <int TABLES, int RG, int WAVES, int EPI>
 hipError_t launch_prefill(const GroupedGemmArgs& a, hipStream_t stream) {
   constexpr int BN = WAVES * RG * 16;
-  static bool attr_set = false;  // one attribute call per instantiation (idempotent)
-  if (!attr_set) {
-    const hipError_t err =
-        hipFuncSetAttribute(reinterpret_cast<const void*>(prefill_gemm_kernel<TABLES, RG, WAVES, EPI>),
-                            hipFuncAttributeMaxDynamicSharedMemorySize, kPrefillLds);
-    if (err != hipSuccess) return err;
-    attr_set = true;
-  }
+  static std::atomic<uint64_t> lds_set{0};
+  const hipError_t err =
+      allow_full_lds(reinterpret_cast<const void*>(prefill_gemm_kernel<TABLES, RG, WAVES, EPI>), lds_set);
+  if (err != hipSuccess) return err;
   const int64_t items = (int64_t)(a.n / BN) * a.max_tiles;
   const int64_t grid = (items + kXcds - 1) / kXcds * kXcds;
   return launch_kernel(prefill_gemm_kernel<TABLES, RG, WAVES, EPI>, dim3((unsigned)grid), dim3(64 * WAVES),
