@@ -271,6 +271,78 @@ def full_layer(work, steps, warmup):
     return start.elapsed_time(stop) / steps * 1e3, shared_bytes, how
 
 
+def mlp_from_logits(work, steps, warmup):
+    """The decode MLP body from router logits (one row; K calls replayed from
+    one HIP graph), both ways: the router kernel then moe_grouped_routes (three
+    launches), and moe_mlp_from_router_logits with the routing inside the decode
+    gate/up kernel (two launches).  Rotated logits, so each call touches its own
+    experts.  Returns {"two_step_us", "fused_us"}."""
+    import torch
+
+    from glm_moe import synthetic as S
+    from glm_moe.contracts import single_gpu_contract
+    from glm_moe.layers.moe.routed_experts import moe_grouped_routes, moe_mlp_from_router_logits
+    from glm_moe.layers.moe.router import route_glm_noaux_tc_logits
+
+    cfg = work.cfg
+    device = work.inputs[0][0].device
+    contract = single_gpu_contract(hidden_size=cfg.hidden, intermediate_size=cfg.intermediate,
+                                   num_experts=cfg.experts, top_k=cfg.top_k)
+    g = torch.Generator(device=device).manual_seed(11)
+    shared = tuple((torch.randn(shape, generator=g, device=device) * 0.02).to(torch.bfloat16)
+                   for shape in ((cfg.intermediate, cfg.hidden), (cfg.intermediate, cfg.hidden),
+                                 (cfg.hidden, cfg.intermediate)))
+    t = work.tables
+    tables = [t[k] for k in TABLE_KEYS]
+    n_rot = len(work.inputs)
+    logits = [torch.from_numpy(S.router_logits(cfg, 1000 + r)).to(device) for r in range(n_rot)]
+    bias = torch.zeros(cfg.experts, dtype=torch.float32, device=device)
+
+    def two_step(i):
+        ids, w = route_glm_noaux_tc_logits(logits[i % n_rot], bias, top_k=cfg.top_k)
+        moe_grouped_routes(work.inputs[i % n_rot][0], ids, w, *tables, contract=contract, shared_bf16=shared)
+
+    def fused(i):
+        moe_mlp_from_router_logits(work.inputs[i % n_rot][0], logits[i % n_rot], bias, *tables, contract=contract,
+                                   shared_bf16=shared)
+
+    result = {}
+    for name, body in (("two_step_us", two_step), ("fused_us", fused)):
+        for i in range(max(warmup, 1)):
+            body(i)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            for i in range(steps):
+                body(warmup + i)
+        for _ in range(GRAPH_WARM_REPLAYS):
+            graph.replay()
+        start = torch.cuda.Event(enable_timing=True)
+        stop = torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        start.record()
+        graph.replay()
+        stop.record()
+        torch.cuda.synchronize()
+        del graph
+        result[name] = start.elapsed_time(stop) / steps * 1e3
+    result["note"] = ("decode MLP body from router logits incl. the resident shared expert: router kernel + "
+                      "moe_grouped_routes, vs routing inside the decode gate/up kernel (glm_moe_moe_layer_from_logits)")
+    return result
+
+
+def with_mlp_from_logits(s, work, steps):
+    cfg = work.cfg
+    if work.activations != "bfloat16" or cfg.tokens != 1 or cfg.experts > 256:
+        return s
+    try:
+        s["mlp_from_logits"] = mlp_from_logits(work, steps, 3)
+    except Exception as exc:  # a secondary figure: report it, keep the headline
+        print(f"[bench] MLP from logits failed: {exc!r}", file=sys.stderr, flush=True)
+        s["mlp_from_logits"] = {"error": repr(exc)}
+    return s
+
+
 def with_full_layer(s, work, steps):
     try:
         us, shared_bytes, how = full_layer(work, steps, 3)
@@ -474,6 +546,7 @@ def main():
 
     with_full_layer(head, work, args.steps)
     with_router(head, cfg, device)
+    with_mlp_from_logits(head, work, args.steps)
     roofline = dominant_roofline(cfg, head)
     if args.copy_calibration:
         copy_calibration(device)
@@ -522,6 +595,7 @@ def main():
         "full_layer_hbm_gbs": head.get("full_layer_hbm_gbs"),
         "full_layer_note": head.get("full_layer_note", head.get("full_layer_error")),
         "router": head["router"],
+        "mlp_from_logits": head.get("mlp_from_logits"),
         "layer_hbm_gbs": head["layer_hbm_gbs"],
         "layer_hbm_frac": head["layer_hbm_gbs"] / HBM_PEAK_GBS,
         "stage_us": head["stage_us"],

@@ -1,6 +1,7 @@
 // Row movement, FP8 table decode and the route combine of the MoE path.
 #include "moe_common.h"
 #include "moe_kernels.h"
+#include "router_wave.h"
 
 namespace glm_moe {
 
@@ -134,30 +135,6 @@ __global__ void combine_routes_kernel(const uint16_t* y, int64_t tokens, int32_t
   }
 }
 
-// Order key of a biased score: the float's bits made monotonic (larger float,
-// larger key), then the complement of the expert id (equal scores: the lower id
-// is larger), so one unsigned 64-bit max picks what lax.top_k picks
-// (router.py:40-42: highest biased score, ties to the lowest id).  NaN scores
-// get the lowest key here and are never chosen ahead of a number (the
-// reference leaves NaN ordering to XLA's sort; this path defines it).
-__device__ __forceinline__ uint64_t router_key(float v, int e) {
-  uint32_t u = __float_as_uint(v);
-  u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
-  if (v != v) u = 0u;
-  return ((uint64_t)u << 32) | (uint32_t)(0xFFFFFFFFu - (uint32_t)e);
-}
-
-__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
-#pragma unroll
-  for (int d = 32; d >= 1; d >>= 1) {
-    const uint32_t lo = __shfl_xor((uint32_t)v, d, 64);
-    const uint32_t hi = __shfl_xor((uint32_t)(v >> 32), d, 64);
-    const uint64_t o = ((uint64_t)hi << 32) | lo;
-    v = o > v ? o : v;
-  }
-  return v;
-}
-
 // GLM noaux_tc routing (glm_tpu/layers/moe/router.py:20-55), one wave per
 // token: FP32 sigmoid scores, selection by score + correction bias, k rounds of
 // a wave-wide arg-max (each lane holds experts lane + 64 j, j < KPER), and the
@@ -169,44 +146,12 @@ __global__ __launch_bounds__(256) void route_noaux_tc_kernel(const float* logits
   const int lane = threadIdx.x & 63;
   const int64_t t = (int64_t)blockIdx.x * (blockDim.x / 64) + (threadIdx.x >> 6);
   if (t >= tokens) return;
-  float score[KPER];
-  uint64_t key[KPER];
-#pragma unroll
-  for (int j = 0; j < KPER; ++j) {
-    const int e = lane + 64 * j;
-    const bool live = e < experts;
-    const float x = live ? logits[t * experts + e] : 0.0f;
-    score[j] = sigmoid_f32(x);
-    key[j] = live ? router_key(score[j] + (bias ? bias[e] : 0.0f), e) : 0ull;
-  }
-  // round r's winner is wave-uniform: lane r keeps it; the sum runs in selection order
-  int my_id = 0;
-  float my_score = 0.0f, sum = 0.0f;
-  for (int r = 0; r < top_k; ++r) {
-    uint64_t best = key[0];
-#pragma unroll
-    for (int j = 1; j < KPER; ++j) best = key[j] > best ? key[j] : best;
-    best = wave_max_u64(best);
-    const int e = (int)(0xFFFFFFFFu - (uint32_t)best);
-    const int owner = e & 63, slot = e >> 6;
-    float sv = score[0];
-#pragma unroll
-    for (int j = 1; j < KPER; ++j) sv = slot == j ? score[j] : sv;
-    const float bs = __shfl(sv, owner, 64);
-    if (lane == r) {
-      my_id = e;
-      my_score = bs;
-    }
-    sum += bs;
-    if (lane == owner) {
-#pragma unroll
-      for (int j = 0; j < KPER; ++j)
-        if (j == slot) key[j] = 0ull;
-    }
-  }
+  int my_id;
+  float my_weight;
+  route_token_noaux<KPER>(logits + t * experts, experts, bias, top_k, lane, my_id, my_weight);
   if (lane < top_k) {
     ids[t * top_k + lane] = my_id;
-    weights[t * top_k + lane] = my_score / sum;
+    weights[t * top_k + lane] = my_weight;
   }
 }
 

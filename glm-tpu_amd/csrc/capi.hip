@@ -163,6 +163,14 @@ float bf16_round_host(float f) {
   return f;
 }
 
+// Routing computed inside the decode gate/up kernel: the router logits
+// [tokens, experts] f32 and the correction bias [experts] (nullable); the
+// route_indices / route_weights of routed_experts_impl are then its outputs.
+struct RouterIn {
+  const float* logits;
+  const float* bias;
+};
+
 int routed_experts_impl(const uint16_t* hidden, int64_t tokens, int64_t hidden_size,
                         const int32_t* route_indices, const float* route_weights, int32_t top_k,
                         int32_t num_experts, int64_t intermediate, const uint8_t* gate_bits,
@@ -170,7 +178,7 @@ int routed_experts_impl(const uint16_t* hidden, int64_t tokens, int64_t hidden_s
                         const uint8_t* down_bits, const float* down_scale, uint32_t flags,
                         const uint16_t* shared, const uint16_t* const* resident, float routed_scale,
                         uint16_t* out, uint8_t* valid, void* workspace, size_t workspace_bytes,
-                        const StageTimer& timer, void* stream_ptr) {
+                        const StageTimer& timer, void* stream_ptr, const RouterIn* router = nullptr) {
   GLM_REQUIRE(tokens > 0 && top_k > 0 && num_experts > 0, "routed experts need tokens, top_k, experts > 0");
   GLM_REQUIRE(top_k <= num_experts, "top_k exceeds expert count");
   GLM_REQUIRE(num_experts <= kMaxExperts, "at most %d experts", kMaxExperts);
@@ -242,6 +250,12 @@ int routed_experts_impl(const uint16_t* hidden, int64_t tokens, int64_t hidden_s
     d.valid = valid;
     d.shared = shared;
     d.routed_scale = routed_scale;
+    if (router != nullptr) {
+      d.router_logits = router->logits;
+      d.router_bias = router->bias;
+      d.ids_out = const_cast<int32_t*>(route_indices);
+      d.weights_out = const_cast<float*>(route_weights);
+    }
     if (resident != nullptr) {
       d.shared_gate = resident[0];
       d.shared_up = resident[1];
@@ -254,6 +268,8 @@ int routed_experts_impl(const uint16_t* hidden, int64_t tokens, int64_t hidden_s
     return GLM_MOE_OK;
   }
 
+  GLM_REQUIRE(router == nullptr, "routing inside the layer runs on decode shapes (at most %d routes)",
+              kMaxDecodeRoutes);
   GLM_REQUIRE(resident == nullptr,
               "the resident shared expert runs on decode shapes (at most %d routes); pass the shared "
               "expert's output to glm_moe_moe_layer instead",
@@ -684,6 +700,40 @@ int glm_moe_moe_layer_resident(const uint16_t* hidden, int64_t tokens, int64_t h
                              num_experts, intermediate, gate_bits, gate_scale, up_bits, up_scale,
                              down_bits, down_scale, flags, nullptr, resident, bf16_round_host(routed_scale), out,
                              valid, workspace, workspace_bytes, StageTimer{nullptr, nullptr}, stream);
+}
+
+int glm_moe_moe_layer_from_logits(const uint16_t* hidden, int64_t tokens, int64_t hidden_size,
+                                  const float* router_logits, const float* correction_bias, int32_t top_k,
+                                  int32_t num_experts, int64_t intermediate, const uint8_t* gate_bits,
+                                  const float* gate_scale, const uint8_t* up_bits, const float* up_scale,
+                                  const uint8_t* down_bits, const float* down_scale, uint32_t flags,
+                                  const uint16_t* shared_gate, const uint16_t* shared_up,
+                                  const uint16_t* shared_down, int64_t shared_intermediate, float routed_scale,
+                                  int32_t* route_indices, float* route_weights, uint16_t* out, uint8_t* valid,
+                                  void* workspace, size_t workspace_bytes, void* stream) {
+  GLM_REQUIRE(router_logits != nullptr && route_indices != nullptr && route_weights != nullptr,
+              "null router logits or route outputs");
+  GLM_REQUIRE(num_experts > 0 && num_experts <= kDecodeRouterExperts,
+              "routing inside the decode kernels takes at most %d experts; route with glm_moe_route_noaux_tc "
+              "and call glm_moe_moe_layer_resident",
+              kDecodeRouterExperts);
+  GLM_REQUIRE(top_k > 0 && top_k <= num_experts, "top_k must be in [1, %d]", (int)num_experts);
+  GLM_REQUIRE(shared_gate && shared_up && shared_down, "null shared-expert table");
+  GLM_REQUIRE(shared_intermediate == intermediate,
+              "the resident shared expert needs the routed experts' intermediate size (%lld), got %lld",
+              (long long)intermediate, (long long)shared_intermediate);
+  GLM_REQUIRE(std::isfinite(routed_scale), "routed scale must be finite");
+  GLM_REQUIRE((flags & GLM_MOE_FP8_ACTIVATIONS) == 0, "the decode layer takes bf16 activations");
+  GLM_REQUIRE(tokens > 0 && uses_decode_path(tokens * top_k, hidden_size, intermediate),
+              "routing inside the layer runs on decode shapes (at most %d routes); route with "
+              "glm_moe_route_noaux_tc and call glm_moe_moe_layer instead",
+              kMaxDecodeRoutes);
+  const uint16_t* resident[3] = {shared_gate, shared_up, shared_down};
+  const RouterIn router{router_logits, correction_bias};
+  return routed_experts_impl(hidden, tokens, hidden_size, route_indices, route_weights, top_k,
+                             num_experts, intermediate, gate_bits, gate_scale, up_bits, up_scale,
+                             down_bits, down_scale, flags, nullptr, resident, bf16_round_host(routed_scale), out,
+                             valid, workspace, workspace_bytes, StageTimer{nullptr, nullptr}, stream, &router);
 }
 
 int glm_moe_event_create(void** event) {

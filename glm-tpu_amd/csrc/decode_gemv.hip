@@ -30,6 +30,7 @@
 // are kept in flight per wave.
 #include "moe_common.h"
 #include "moe_kernels.h"
+#include "router_wave.h"
 
 namespace glm_moe {
 
@@ -436,7 +437,24 @@ void decode_gate_up_kernel(const DecodeArgs a, int wave_steps) {
     return;
   }
   DecodeRoute rt;
-  if (!decode_route(a.ids, a.routes, a.experts, a.drop_unowned, blockIdx.x, rt)) return;
+  if (a.router_logits != nullptr) {
+    // route j = t * top_k + s of token t: every wave routes the token itself
+    // (top-k ids are distinct and in range, so every route is active); the
+    // token's first-slot workgroup of row block 0 publishes ids and weights
+    const int j = blockIdx.x, t = j / a.top_k, s = j % a.top_k;
+    int my_id;
+    float my_weight;
+    route_token_noaux<kDecodeRouterExperts / 64>(a.router_logits + (int64_t)t * a.experts, a.experts, a.router_bias,
+                                                 a.top_k, lane, my_id, my_weight);
+    rt.route = j;
+    rt.expert = uniform(__shfl(my_id, s, 64));
+    if (s == 0 && blockIdx.y == 0 && wk == 0 && lane < a.top_k) {
+      a.ids_out[j + lane] = my_id;
+      a.weights_out[j + lane] = my_weight;
+    }
+  } else if (!decode_route(a.ids, a.routes, a.experts, a.drop_unowned, blockIdx.x, rt)) {
+    return;
+  }
   const int steps = (H + kStepK - 1) / kStepK;
   GemvStream<2> g;
   g.k = H;
@@ -610,6 +628,10 @@ hipError_t launch_decode_routed(const DecodeArgs& a, hipStream_t stream, const L
   const int gu_steps = gate_up_wave_steps(a.hidden);
   const size_t gu_lds = sizeof(float) * kGateUpWaves * 2 * kGemvRows +
                         sizeof(uint16_t) * kGateUpWaves * xs_elems(gu_steps);
+  if (a.router_logits != nullptr &&
+      (a.experts > kDecodeRouterExperts || a.top_k > 64 || a.ids_out == nullptr || a.weights_out == nullptr ||
+       a.ids != a.ids_out || a.weights != a.weights_out))
+    return hipErrorInvalidValue;
   const bool resident = a.shared_gate != nullptr;
   if (resident && (a.shared_up == nullptr || a.shared_down == nullptr || a.act_shared == nullptr ||
                    bf16_wave_steps(a.hidden, kGateUpWaves) * kBf16StepK > xs_elems(gu_steps) ||

@@ -187,7 +187,17 @@ struct DecodeArgs {
   const uint16_t* shared_up;   // [intermediate, hidden] bf16
   const uint16_t* shared_down; // [hidden, intermediate] bf16
   uint16_t* act_shared;        // workspace [tokens, intermediate] bf16
+  // routing inside the gate/up kernel (null: ids / weights are inputs): each
+  // workgroup routes its token from the router logits [tokens, experts] f32
+  // (+ correction bias [experts], nullable); the first slot's workgroups write
+  // the token's ids and weights to ids_out / weights_out, which ids / weights
+  // then point to for the down kernel.  experts <= kDecodeRouterExperts.
+  const float* router_logits;
+  const float* router_bias;
+  int32_t* ids_out;
+  float* weights_out;
 };
+constexpr int kDecodeRouterExperts = 256;
 // The decode kernels stage one wave's K range (<= 2048) in LDS: hidden <= 8192
 // (four waves split it), intermediate <= 2048.
 bool decode_path_fits(int64_t hidden, int64_t intermediate);

@@ -1,0 +1,81 @@
+// GLM noaux_tc routing of one token by one wave (reference
+// glm_tpu/layers/moe/router.py:20-55), shared by the router kernel and the
+// decode gate/up kernel that routes its own token, so both give the same bits.
+#pragma once
+
+#include "moe_common.h"
+
+namespace glm_moe {
+
+// Order key of a biased score: the float's bits made monotonic (larger float,
+// larger key), then the complement of the expert id (equal scores: the lower id
+// is larger), so one unsigned 64-bit max picks what lax.top_k picks
+// (router.py:40-42: highest biased score, ties to the lowest id).  NaN scores
+// get the lowest key here and are never chosen ahead of a number (the
+// reference leaves NaN ordering to XLA's sort; this path defines it).
+__device__ __forceinline__ uint64_t router_key(float v, int e) {
+  uint32_t u = __float_as_uint(v);
+  u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+  if (v != v) u = 0u;
+  return ((uint64_t)u << 32) | (uint32_t)(0xFFFFFFFFu - (uint32_t)e);
+}
+
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
+#pragma unroll
+  for (int d = 32; d >= 1; d >>= 1) {
+    const uint32_t lo = __shfl_xor((uint32_t)v, d, 64);
+    const uint32_t hi = __shfl_xor((uint32_t)(v >> 32), d, 64);
+    const uint64_t o = ((uint64_t)hi << 32) | lo;
+    v = o > v ? o : v;
+  }
+  return v;
+}
+
+// One token: FP32 sigmoid scores of its `experts` logits, selection by score +
+// correction bias (nullable), k rounds of a wave-wide arg-max (lane l holds
+// experts l + 64 j, j < KPER, so experts <= 64 * KPER), and the selected
+// *unbiased* scores renormalised in FP32 in selection order.  Lane r < top_k
+// gets the r-th selected expert and its weight; the other lanes get expert 0
+// and an unspecified weight.  Every lane of the wave must call it.
+template <int KPER>
+__device__ __forceinline__ void route_token_noaux(const float* logits_row, int experts, const float* bias, int top_k,
+                                                  int lane, int& my_id, float& my_weight) {
+  float score[KPER];
+  uint64_t key[KPER];
+#pragma unroll
+  for (int j = 0; j < KPER; ++j) {
+    const int e = lane + 64 * j;
+    const bool live = e < experts;
+    const float x = live ? logits_row[e] : 0.0f;
+    score[j] = sigmoid_f32(x);
+    key[j] = live ? router_key(score[j] + (bias ? bias[e] : 0.0f), e) : 0ull;
+  }
+  // round r's winner is wave-uniform: lane r keeps it; the sum runs in selection order
+  my_id = 0;
+  float my_score = 0.0f, sum = 0.0f;
+  for (int r = 0; r < top_k; ++r) {
+    uint64_t best = key[0];
+#pragma unroll
+    for (int j = 1; j < KPER; ++j) best = key[j] > best ? key[j] : best;
+    best = wave_max_u64(best);
+    const int e = (int)(0xFFFFFFFFu - (uint32_t)best);
+    const int owner = e & 63, slot = e >> 6;
+    float sv = score[0];
+#pragma unroll
+    for (int j = 1; j < KPER; ++j) sv = slot == j ? score[j] : sv;
+    const float bs = __shfl(sv, owner, 64);
+    if (lane == r) {
+      my_id = e;
+      my_score = bs;
+    }
+    sum += bs;
+    if (lane == owner) {
+#pragma unroll
+      for (int j = 0; j < KPER; ++j)
+        if (j == slot) key[j] = 0ull;
+    }
+  }
+  my_weight = my_score / sum;
+}
+
+}  // namespace glm_moe

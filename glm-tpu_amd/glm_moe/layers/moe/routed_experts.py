@@ -433,3 +433,87 @@ def moe_grouped_routes(
         routed_scale=contract.routed_scaling_factor, **shared_kw,
     )
     return output
+
+
+def moe_mlp_from_router_logits(
+    hidden_local: torch.Tensor,
+    router_logits: torch.Tensor,
+    correction_bias: torch.Tensor | None,
+    expert_gate_bits_local: torch.Tensor,
+    expert_gate_scale_local: torch.Tensor,
+    expert_up_bits_local: torch.Tensor,
+    expert_up_scale_local: torch.Tensor,
+    expert_down_bits_local: torch.Tensor,
+    expert_down_scale_local: torch.Tensor,
+    *,
+    contract: GlmMoeNumericalContract = single_gpu_contract(),
+    shared_bf16: tuple[Any, Any, Any],
+) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """The decode MoE MLP body of one row from its router logits:
+    ``(update, route_indices, route_weights)``.
+
+    The reference's decode MLP (``glm_tpu/models/glm_moe_dsa/decoder_layer.py:636-656``)
+    routes the row (``route_glm_noaux_tc_logits``, ``router.py:20-55``, the last
+    step of ``router_from_shards``) and runs ``moe_grouped_routes`` on the
+    selection, returning both.  Here, on the shapes the decode kernels take
+    (``uses_decode_kernels``, at most 256 experts), the gate/up kernel routes its
+    token itself (``glm_moe_moe_layer_from_logits``: one launch fewer, ids and
+    weights bit-equal to the router kernel's); otherwise the router kernel runs
+    first, then ``moe_grouped_routes``.
+    """
+    from glm_moe.layers.moe.router import route_glm_noaux_tc_logits
+
+    experts, top_k = contract.local_experts, contract.top_k
+    if router_logits.ndim != 2 or tuple(router_logits.shape) != (hidden_local.shape[0], experts):
+        raise ValueError(f"router_logits must have shape {(hidden_local.shape[0], experts)}")
+    if correction_bias is not None and tuple(correction_bias.shape) != (experts,):
+        raise ValueError(f"correction_bias must have shape {(experts,)}")
+    inter, h = contract.intermediate_size, contract.hidden_size
+    fused = (
+        hidden_local.ndim == 2 and hidden_local.shape[0] == 1 and experts <= 256
+        and uses_decode_kernels(1, top_k, h, inter)
+    )
+    if not fused:
+        bias = correction_bias if correction_bias is not None else torch.zeros(
+            experts, dtype=torch.float32, device=router_logits.device)
+        ids, weights = route_glm_noaux_tc_logits(router_logits, bias, top_k=top_k)
+        update = moe_grouped_routes(
+            hidden_local, ids, weights, expert_gate_bits_local, expert_gate_scale_local, expert_up_bits_local,
+            expert_up_scale_local, expert_down_bits_local, expert_down_scale_local, contract=contract,
+            shared_bf16=shared_bf16)
+        return update, ids, weights
+    ids = torch.empty((1, top_k), dtype=torch.int32, device=hidden_local.device)
+    weights = torch.empty((1, top_k), dtype=torch.float32, device=hidden_local.device)
+    _check_layer_shapes(hidden_local, ids, weights, expert_gate_bits_local, expert_up_bits_local,
+                        expert_down_bits_local, contract, rows_exact=1)
+    if (
+        len(shared_bf16) != 3
+        or any(t.dtype != torch.bfloat16 for t in shared_bf16)
+        or tuple(shared_bf16[0].shape) != (inter, h)
+        or tuple(shared_bf16[1].shape) != (inter, h)
+        or tuple(shared_bf16[2].shape) != (h, inter)
+    ):
+        raise ValueError("grouped MoE BF16 shared tables drifted")
+    for scale, rows, cols in ((expert_gate_scale_local, inter, h), (expert_up_scale_local, inter, h),
+                              (expert_down_scale_local, h, inter)):
+        if scale.dtype != torch.float32 or tuple(scale.shape) != (experts, rows // 128, cols // 128):
+            raise ValueError("expert scales must be float32 [E, N/128, K/128]")
+    tables = tuple(t.contiguous() for t in shared_bf16)
+    logits = router_logits.float().contiguous()
+    bias = None if correction_bias is None else correction_bias.float().contiguous()
+    _lib.require_device(hidden_local, logits, bias, expert_gate_bits_local, expert_gate_scale_local,
+                        expert_up_bits_local, expert_up_scale_local, expert_down_bits_local,
+                        expert_down_scale_local, *tables)
+    out = torch.empty((1, h), dtype=torch.bfloat16, device=hidden_local.device)
+    valid = torch.empty((), dtype=torch.bool, device=hidden_local.device)
+    ws = routed_workspace(1, top_k, experts, h, inter, hidden_local.device)
+    flags = _lib.ROUTE_SUM_BF16 | _lib.DROP_UNOWNED  # moe_grouped_routes' body (routed_experts.py:250-253, :293)
+    _lib.call(
+        "glm_moe_moe_layer_from_logits", _lib.ptr(hidden_local.contiguous()), 1, h, _lib.ptr(logits),
+        _lib.ptr(bias), top_k, experts, inter, _lib.ptr(expert_gate_bits_local), _lib.ptr(expert_gate_scale_local),
+        _lib.ptr(expert_up_bits_local), _lib.ptr(expert_up_scale_local), _lib.ptr(expert_down_bits_local),
+        _lib.ptr(expert_down_scale_local), flags, *(_lib.ptr(t) for t in tables), inter,
+        float(contract.routed_scaling_factor), _lib.ptr(ids), _lib.ptr(weights), _lib.ptr(out), _lib.ptr(valid),
+        _lib.ptr(ws), ws.numel(), _lib.stream_of(hidden_local),
+    )
+    return out, ids, weights

@@ -227,6 +227,29 @@ int glm_moe_moe_layer_resident(const uint16_t* hidden, int64_t tokens, int64_t h
                                uint16_t* out, uint8_t* valid, void* workspace, size_t workspace_bytes,
                                void* stream);
 
+/* The decode MoE MLP from router logits, in the same two launches as
+ * glm_moe_moe_layer_resident: the noaux_tc routing of
+ * glm_moe_route_noaux_tc (route_glm_noaux_tc_logits,
+ * glm_tpu/layers/moe/router.py:20-55) is computed inside the gate/up kernel,
+ * each workgroup for its own token, instead of in a launch of its own; then the
+ * layer of glm_moe_moe_layer_resident.  Replaces the composition of the
+ * reference's decode MLP body, router then moe_grouped_routes
+ * (glm_tpu/models/glm_moe_dsa/decoder_layer.py:636-656), from the router
+ * logits on.  router_logits [tokens, num_experts] f32, correction_bias
+ * [num_experts] f32 (nullable: zero); route_indices / route_weights
+ * [tokens, top_k] are outputs (the selected ids and renormalised weights,
+ * bit-equal to glm_moe_route_noaux_tc's).  Decode shapes only, at most 256
+ * experts.  Same workspace as glm_moe_routed_experts. */
+int glm_moe_moe_layer_from_logits(const uint16_t* hidden, int64_t tokens, int64_t hidden_size,
+                                  const float* router_logits, const float* correction_bias, int32_t top_k,
+                                  int32_t num_experts, int64_t intermediate, const uint8_t* gate_bits,
+                                  const float* gate_scale, const uint8_t* up_bits, const float* up_scale,
+                                  const uint8_t* down_bits, const float* down_scale, uint32_t flags,
+                                  const uint16_t* shared_gate, const uint16_t* shared_up,
+                                  const uint16_t* shared_down, int64_t shared_intermediate, float routed_scale,
+                                  int32_t* route_indices, float* route_weights, uint16_t* out, uint8_t* valid,
+                                  void* workspace, size_t workspace_bytes, void* stream);
+
 /* Synthetic FP8 expert tables for tests and benchmarks, the reference's fixture
  * recipe (tools/equivalence/fixture.py:158-172) with 128x128 block scales:
  * w ~ N(0, sigma) (counter-based hash + Box-Muller), scale = amax/448 per block,

@@ -648,3 +648,107 @@ def test_router_matches_oracle(device, tokens, experts, top_k, zipf, biased):
     assert clear.mean() > 0.95
     np.testing.assert_array_equal(ids.cpu().numpy()[clear], ref_ids[clear])
     np.testing.assert_allclose(w.cpu().numpy()[clear], ref_w[clear], rtol=2e-6, atol=1e-7)
+
+
+# ----------------------------------------------------------------------------- routing inside the decode layer
+# glm_moe_moe_layer_from_logits routes each token inside the decode gate/up
+# kernel.  It must give the router kernel's ids and weights and the two-step
+# layer's output (route_glm_noaux_tc_logits, then the resident layer), bit for bit.
+def _router_layer_case(tokens, experts, hidden, inter, top_k, seed, device, biased=True):
+    rng = np.random.default_rng(seed)
+    cfg, x, _, _, tables = _small_case(tokens, experts, hidden, inter, top_k, 0.0, seed=seed)
+    logits = rng.standard_normal((tokens, experts)).astype(np.float32)
+    bias = (rng.standard_normal(experts) * 0.1).astype(np.float32) if biased else np.zeros(experts, np.float32)
+    shared_f32 = [(rng.standard_normal(shape) * std).astype(np.float32)
+                  for shape, std in (((inter, hidden), hidden ** -0.5), ((inter, hidden), hidden ** -0.5),
+                                     ((hidden, inter), 2 * inter ** -0.5))]
+    return (cfg, x, logits, bias, tables, _device_tables(tables, device), shared_f32,
+            [bf16_dev(a, device) for a in shared_f32])
+
+
+def _layer_from_logits_abi(x_dev, logits_dev, bias_dev, t, shared_dev, top_k, flags, device):
+    from glm_moe import _lib
+    from glm_moe.layers.moe.routed_experts import routed_workspace
+
+    tokens, hidden = x_dev.shape
+    experts, inter = t["gate_bits"].shape[0], t["gate_bits"].shape[1]
+    ids = torch.full((tokens, top_k), -7, dtype=torch.int32, device=device)
+    w = torch.full((tokens, top_k), -1.0, dtype=torch.float32, device=device)
+    out = torch.empty((tokens, hidden), dtype=torch.bfloat16, device=device)
+    valid = torch.empty((), dtype=torch.bool, device=device)
+    ws = routed_workspace(tokens, top_k, experts, hidden, inter, device)
+    _lib.call("glm_moe_moe_layer_from_logits", _lib.ptr(x_dev), tokens, hidden, _lib.ptr(logits_dev),
+              _lib.ptr(bias_dev), top_k, experts, inter, *(_lib.ptr(t[k]) for k in TABLE_KEYS), flags,
+              *(_lib.ptr(s) for s in shared_dev), inter, 2.5, _lib.ptr(ids), _lib.ptr(w), _lib.ptr(out),
+              _lib.ptr(valid), _lib.ptr(ws), ws.numel(), _lib.stream_of(x_dev))
+    return out, ids, w, valid
+
+
+@pytest.mark.parametrize("tokens,experts,hidden,inter,top_k,bf16_sum", [
+    (1, 256, 512, 256, 8, True),      # the decode body (bf16 route sum)
+    (4, 256, 768, 384, 8, False),     # four tokens, FP32 route sum
+    (8, 64, 512, 256, 8, True),       # 64 routes, the decode kernels' limit; 64 experts
+    (3, 8, 256, 256, 2, False),       # the toy geometry
+])
+def test_layer_from_router_logits_equals_two_steps(device, tokens, experts, hidden, inter, top_k, bf16_sum):
+    from glm_moe import _lib
+    from glm_moe.layers.moe.routed_experts import routed_experts
+    from glm_moe.layers.moe.router import route_glm_noaux_tc_logits
+
+    cfg, x, logits, bias, tables, t, shared_f32, shared_dev = _router_layer_case(
+        tokens, experts, hidden, inter, top_k, tokens * 31 + experts, device)
+    x_dev, logits_dev, bias_dev = bf16_dev(x, device), dev(logits, device), dev(bias, device)
+    flags = _lib.ROUTE_SUM_BF16 if bf16_sum else 0
+    out, ids, w, ok = _layer_from_logits_abi(x_dev, logits_dev, bias_dev, t, shared_dev, top_k, flags, device)
+    ref_ids, ref_w = route_glm_noaux_tc_logits(logits_dev, bias_dev, top_k=top_k)
+    np.testing.assert_array_equal(ids.cpu().numpy(), ref_ids.cpu().numpy())
+    np.testing.assert_array_equal(w.cpu().numpy().view(np.uint32), ref_w.cpu().numpy().view(np.uint32))
+    kw = dict(route_sum="bfloat16" if bf16_sum else "float32", check_weights=False)
+    ref, ref_ok = routed_experts(x_dev, ref_ids, ref_w, *(t[k] for k in TABLE_KEYS), shared_tables=tuple(shared_dev),
+                                 **kw)
+    assert bool(ok) and bool(ref_ok)
+    np.testing.assert_array_equal(bf16_bits_of(out), bf16_bits_of(ref))
+    # and against the oracle: its router, then its layer
+    o_ids, o_w = O.route_glm_noaux_tc_logits(logits, bias, top_k=top_k)
+    np.testing.assert_array_equal(ids.cpu().numpy(), o_ids)
+    o_out, _ = O.moe_layer(x, o_ids, o_w, **tables, shared_gate=shared_f32[0], shared_up=shared_f32[1],
+                           shared_down=shared_f32[2], decode=bf16_sum)
+    print(cfg, "vs oracle:", assert_moe_close(host_f32(out), o_out))
+
+
+def test_layer_from_router_logits_known_answers_and_python_api(device):
+    """Router KATs (tests/layers/moe/test_router.py:61-65: equal logits -> ids 0..7,
+    weights 1/8) through the fused layer, and the Python decode MLP body on both
+    of its paths (fused on decode shapes, router kernel + moe_grouped_routes otherwise)."""
+    from glm_moe.contracts import single_gpu_contract
+    from glm_moe.layers.moe.routed_experts import moe_grouped_routes, moe_mlp_from_router_logits
+    from glm_moe.layers.moe.router import route_glm_noaux_tc_logits
+
+    cfg, x, logits, bias, tables, t, shared_f32, shared_dev = _router_layer_case(1, 256, 512, 256, 8, 77, device)
+    x_dev = bf16_dev(x, device)
+    zeros = torch.zeros((1, 256), dtype=torch.float32, device=device)
+    _, ids, w, ok = _layer_from_logits_abi(x_dev, zeros, None, t, shared_dev, 8, 0, device)
+    assert bool(ok)
+    np.testing.assert_array_equal(ids.cpu().numpy(), [list(range(8))])
+    np.testing.assert_array_equal(w.cpu().numpy(), np.full((1, 8), 0.125, np.float32))
+    contract = single_gpu_contract(hidden_size=512, intermediate_size=256, num_experts=256, top_k=8)
+    logits_dev, bias_dev = dev(logits, device), dev(bias, device)
+    tabs = [t[k] for k in TABLE_KEYS]
+    update, ids, w = moe_mlp_from_router_logits(x_dev, logits_dev, bias_dev, *tabs, contract=contract,
+                                                shared_bf16=tuple(shared_dev))
+    ref_ids, ref_w = route_glm_noaux_tc_logits(logits_dev, bias_dev, top_k=8)
+    np.testing.assert_array_equal(ids.cpu().numpy(), ref_ids.cpu().numpy())
+    np.testing.assert_array_equal(w.cpu().numpy(), ref_w.cpu().numpy())
+    ref = moe_grouped_routes(x_dev, ref_ids, ref_w, *tabs, contract=contract, shared_bf16=tuple(shared_dev))
+    np.testing.assert_array_equal(bf16_bits_of(update), bf16_bits_of(ref))
+    # more experts than the in-kernel router takes: router kernel, then the layer
+    contract = single_gpu_contract(hidden_size=512, intermediate_size=256, num_experts=512, top_k=8)
+    cfg, x, logits, bias, tables, t, shared_f32, shared_dev = _router_layer_case(1, 512, 512, 256, 8, 78, device)
+    x_dev, logits_dev, bias_dev = bf16_dev(x, device), dev(logits, device), dev(bias, device)
+    tabs = [t[k] for k in TABLE_KEYS]
+    update, ids, w = moe_mlp_from_router_logits(x_dev, logits_dev, bias_dev, *tabs, contract=contract,
+                                                shared_bf16=tuple(shared_dev))
+    ref_ids, ref_w = route_glm_noaux_tc_logits(logits_dev, bias_dev, top_k=8)
+    np.testing.assert_array_equal(ids.cpu().numpy(), ref_ids.cpu().numpy())
+    ref = moe_grouped_routes(x_dev, ref_ids, ref_w, *tabs, contract=contract, shared_bf16=tuple(shared_dev))
+    np.testing.assert_array_equal(bf16_bits_of(update), bf16_bits_of(ref))

@@ -117,6 +117,20 @@ def test_static_refusals_raise_value_error_through_the_abi():
                                             1 << 30, null)
     with pytest.raises(ValueError, match="intermediate size"):
         _lib.check(status)
+    # routing inside the decode layer: logits and route outputs required, <= 256 experts, decode shapes
+    def from_logits(tokens, experts, logits, ids):
+        return lib.glm_moe_moe_layer_from_logits(fake, tokens, 6144, logits, null, 8, experts, 2048, fake, fake, fake,
+                                                 fake, fake, fake, 0, fake, fake, fake, 2048, ctypes.c_float(2.5),
+                                                 ids, fake, fake, fake, fake, 1 << 30, null)
+
+    with pytest.raises(ValueError, match="null router logits"):
+        _lib.check(from_logits(1, 256, null, fake))
+    with pytest.raises(ValueError, match="null router logits"):
+        _lib.check(from_logits(1, 256, fake, null))
+    with pytest.raises(ValueError, match="at most 256 experts"):
+        _lib.check(from_logits(1, 512, fake, fake))
+    with pytest.raises(ValueError, match="decode shapes"):
+        _lib.check(from_logits(300, 256, fake, fake))
     assert lib.glm_moe_uses_decode_kernels(1, 8, 6144, 2048) == 1
     assert lib.glm_moe_uses_decode_kernels(9, 8, 6144, 2048) == 0
     assert lib.glm_moe_uses_decode_kernels(8, 8, 6144, 4096) == 0
