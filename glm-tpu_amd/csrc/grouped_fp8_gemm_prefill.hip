@@ -147,12 +147,6 @@ __global__ __launch_bounds__(64 * WAVES, 1) void prefill_gemm_kernel(const Group
   item_of_expert(item - stripes * t0, stripes, nt, stripe, tile);
   tile += t0;
   if (stripe < 0 || stripe >= stripes || tile >= a.max_tiles) return;
-  const int r0 = uniform(a.tile_row[tile]);
-  const int live = uniform(a.tile_live[tile]);
-  // A consistent plan always passes; a corrupt one computes nothing instead of
-  // reading out of bounds.
-  if (uniform(a.tile_expert[tile]) != e || r0 < 0 || live <= 0 || live > kBM || r0 + live > a.rows) return;
-  const int ncg = (live + 15) >> 4;
 
   const int lane = threadIdx.x & 63;
   const int wave = uniform(threadIdx.x >> 6);
@@ -182,6 +176,27 @@ __global__ __launch_bounds__(64 * WAVES, 1) void prefill_gemm_kernel(const Group
     sreg[g] = lane < KB ? srow[lane] : 0.0f;
   }
   const int woff = (lane >> 3) * K + (((lane & 7) ^ (lane >> 3)) << 4);
+  uint8_t* const wring = lds + wave * WAVE_BLOCK;  // ring slot s at + s * 32 KB
+  // Weight blocks 0 and 1 (slots 0 and 1 of every variant's ring) go out before
+  // the tile's rows are known: their HBM latency covers the tile and row-id
+  // loads that the activation loads wait for.
+#pragma unroll
+  for (int blk = 0; blk < 2; ++blk)
+#pragma unroll
+    for (int g = 0; g < GROUPS; ++g)
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+        load_lds_16<kNonTemporal>(wrsrc[g], wring + blk * kStripeBlockBytes + (2 * g + h) * 1024,
+                                  blk < KB ? woff + 8 * h * K : kOutOfRange, blk < KB ? blk * kScaleBlock : 0);
+  const int r0 = uniform(a.tile_row[tile]);
+  const int live = uniform(a.tile_live[tile]);
+  // A consistent plan always passes; a corrupt one computes nothing instead of
+  // reading out of bounds.
+  if (uniform(a.tile_expert[tile]) != e || r0 < 0 || live <= 0 || live > kBM || r0 + live > a.rows) {
+    wait_all_loads();  // no load may still target LDS when the workgroup ends
+    return;
+  }
+  const int ncg = (live + 15) >> 4;
   const __amdgpu_buffer_rsrc_t xrsrc = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<uint16_t*>(a.x), (short)0, (int)(a.x_rows * K * 2), kBufferFormat);
 
@@ -204,9 +219,9 @@ __global__ __launch_bounds__(64 * WAVES, 1) void prefill_gemm_kernel(const Group
     constexpr int XSTAGE = Rings::XSTAGE;
     static_assert(XSTAGE >= NCG * 16 * kRowBytes, "activation stage holds the tile's rows");
     static_assert(SW * kStripeBlockBytes + SX * XSTAGE <= kPrefillLds, "LDS budget");
+    static_assert(SW >= 3, "weight blocks 0 and 1 are in flight before the variant is chosen");
     constexpr int PENDING = prefill_pending(SW, SX, XLOADS, WLOADS);
     static_assert(PENDING >= 0 && PENDING < 64, "vmcnt range");
-    uint8_t* const wring = lds + wave * WAVE_BLOCK;     // slot s at + s * 32 KB
     uint8_t* const xring = lds + SW * kStripeBlockBytes;  // stage s at + s * XSTAGE
 
     // activation rows this lane loads: instruction i covers rows 4 * (wave *
@@ -241,17 +256,31 @@ __global__ __launch_bounds__(64 * WAVES, 1) void prefill_gemm_kernel(const Group
                       in ? blk * kScaleBlock : 0);
     };
 
+    // output rows of this lane's route columns, loaded ahead of the streams so
+    // the epilogue waits at most for the weighted epilogue's route weights
+    int orow[NCG];
+#pragma unroll
+    for (int cg = 0; cg < NCG; ++cg) {
+      const int col = cg * 16 + lrow;
+      orow[cg] = col < live ? (int)fragment_row(a, r0 + col) : -1;
+    }
+
     // prologue: the issue schedule's iterations -P .. -1
     constexpr int P = (SX > SW ? SX : SW) - 1;
 #pragma unroll
     for (int i = -P; i < 0; ++i) {
       if (i + SX - 1 >= 0) issue_x(i + SX - 1);
-      if (i + SW - 1 >= 0) issue_w(i + SW - 1);
+      if (i + SW - 1 >= 2) issue_w(i + SW - 1);  // blocks 0 and 1 went out first
     }
     for (int kb = 0; kb < KB; ++kb) {
       // this wave's loads of block kb have landed; after the barrier everyone's
-      // have, and everyone is done with block kb - 1, whose slots are refilled now
-      wait_loads_then_barrier<PENDING>();
+      // have, and everyone is done with block kb - 1, whose slots are refilled now.
+      // Block 0 waits for every prologue load (weights 0 and 1 were issued ahead
+      // of the schedule); from block 1 on the schedule's count holds.
+      if (kb == 0)
+        wait_loads_then_barrier<0>();
+      else
+        wait_loads_then_barrier<PENDING>();
       issue_x(kb + SX - 1);
       issue_w(kb + SW - 1);
 
@@ -315,14 +344,15 @@ __global__ __launch_bounds__(64 * WAVES, 1) void prefill_gemm_kernel(const Group
     wait_all_loads();  // no load may still target LDS when the workgroup ends
 
     // Epilogue: lane holds rows n .. n+3 of route column cg*16 + lrow.
+    float wgt[NCG];  // every route weight load in flight at once
 #pragma unroll
-    for (int cg = 0; cg < NCG; ++cg) {
-      const int col = cg * 16 + lrow;
-      if (col >= live) continue;
+    for (int cg = 0; cg < NCG; ++cg) wgt[cg] = fragment_weight<EPI>(a, orow[cg]);
+#pragma unroll
+    for (int cg = 0; cg < NCG; ++cg)
 #pragma unroll
       for (int rg = 0; rg < RG; ++rg)
-        store_fragment<TABLES, EPI>(a, r0 + col, n0 + rg * 16 + lgrp * 4, acc[0][rg][cg], acc[TABLES - 1][rg][cg]);
-    }
+        store_fragment_at<TABLES, EPI>(a, orow[cg], wgt[cg], n0 + rg * 16 + lgrp * 4, acc[0][rg][cg],
+                                       acc[TABLES - 1][rg][cg]);
   };
   switch (ncg) {
     case 1: run(std::integral_constant<int, 1>{}); break;
@@ -491,6 +521,12 @@ __global__ __launch_bounds__(64 * WAVES, 1) void prefill_gemm_fp8_kernel(const G
                       in ? blk * kScaleBlock : 0);
     };
 
+    int orow[NCG];  // as in the bf16 kernel: output rows loaded ahead of the streams
+#pragma unroll
+    for (int cg = 0; cg < NCG; ++cg) {
+      const int col = cg * 16 + lrow;
+      orow[cg] = col < live ? (int)fragment_row(a, r0 + col) : -1;
+    }
     constexpr int P = (SX > SW ? SX : SW) - 1;
 #pragma unroll
     for (int i = -P; i < 0; ++i) {
@@ -536,14 +572,15 @@ __global__ __launch_bounds__(64 * WAVES, 1) void prefill_gemm_fp8_kernel(const G
       }
     }
     wait_all_loads();
+    float wgt[NCG];  // every route weight load in flight at once
 #pragma unroll
-    for (int cg = 0; cg < NCG; ++cg) {
-      const int col = cg * 16 + lrow;
-      if (col >= live) continue;
+    for (int cg = 0; cg < NCG; ++cg) wgt[cg] = fragment_weight<EPI>(a, orow[cg]);
+#pragma unroll
+    for (int cg = 0; cg < NCG; ++cg)
 #pragma unroll
       for (int rg = 0; rg < RG; ++rg)
-        store_fragment<TABLES, EPI>(a, r0 + col, n0 + rg * 16 + lgrp * 4, acc[0][rg][cg], acc[TABLES - 1][rg][cg]);
-    }
+        store_fragment_at<TABLES, EPI>(a, orow[cg], wgt[cg], n0 + rg * 16 + lgrp * 4, acc[0][rg][cg],
+                                       acc[TABLES - 1][rg][cg]);
   };
   switch (ncg) {
     case 1: run(std::integral_constant<int, 1>{}); break;

@@ -58,3 +58,37 @@ def test_graph_replays_match_eager(tokens, experts, hidden, inter, top_k, mode):
         torch.cuda.synchronize()
         assert torch.equal(out, eager), f"replay {replay} differs from the eager result"
         assert bool(valid) == bool(ok)
+
+
+@pytest.mark.gpu
+def test_graph_replays_of_the_layer_from_router_logits_match_eager():
+    """The decode MLP body routed inside the gate/up kernel: replayed ids, weights
+    and output equal the eager call's, with other eager calls between replays."""
+    from glm_moe.contracts import single_gpu_contract
+    from glm_moe.layers.moe.routed_experts import moe_mlp_from_router_logits
+
+    x, _, _, tables = _case(1, 256, 512, 256, 8, seed=21)
+    contract = single_gpu_contract(hidden_size=512, intermediate_size=256, num_experts=256, top_k=8)
+    g = torch.Generator(device="cuda").manual_seed(2)
+    shared = tuple((torch.randn(s, generator=g, device="cuda") * 0.05).to(torch.bfloat16)
+                   for s in ((256, 512), (256, 512), (512, 256)))
+    logits = torch.randn((1, 256), generator=g, device="cuda")
+    logits2 = torch.randn((1, 256), generator=g, device="cuda")
+    bias = torch.randn(256, generator=g, device="cuda") * 0.1
+    eager = [t.clone() for t in moe_mlp_from_router_logits(x, logits, bias, *tables, contract=contract,
+                                                           shared_bf16=shared)]
+    other = [t.clone() for t in moe_mlp_from_router_logits(x, logits2, bias, *tables, contract=contract,
+                                                           shared_bf16=shared)]
+    assert not torch.equal(eager[1], other[1])
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        captured = moe_mlp_from_router_logits(x, logits, bias, *tables, contract=contract, shared_bf16=shared)
+    for replay in range(3):
+        again = moe_mlp_from_router_logits(x, logits2, bias, *tables, contract=contract, shared_bf16=shared)
+        torch.cuda.synchronize()
+        assert all(torch.equal(a, b) for a, b in zip(again, other))
+        graph.replay()
+        torch.cuda.synchronize()
+        for got, want in zip(captured, eager):
+            assert torch.equal(got, want), f"replay {replay} differs from the eager result"
