@@ -426,11 +426,6 @@ __global__ __launch_bounds__(64 * WAVES, 1) void prefill_gemm_fp8_kernel(const G
   item_of_expert(item - stripes * t0, stripes, nt, stripe, tile);
   tile += t0;
   if (stripe < 0 || stripe >= stripes || tile >= a.max_tiles) return;
-  const int r0 = uniform(a.tile_row[tile]);
-  const int live = uniform(a.tile_live[tile]);
-  if (uniform(a.tile_expert[tile]) != e || r0 < 0 || live <= 0 || live > kBM || r0 + live > a.rows) return;
-  const int ncg = (live + 15) >> 4;
-
   const int lane = threadIdx.x & 63;
   const int wave = uniform(threadIdx.x >> 6);
   const int lrow = lane & 15;
@@ -439,11 +434,6 @@ __global__ __launch_bounds__(64 * WAVES, 1) void prefill_gemm_fp8_kernel(const G
   const int K = a.k;
   const int KB = K / kScaleBlock;
   const int n0 = stripe * BN + wave * RG * 16;
-  auto phys_row = [&](int row) -> int64_t {
-    const int r = r0 + (row < live ? row : 0);  // padding rows repeat a live row; their columns are dropped
-    int64_t phys = a.x_row_ids ? a.x_row_ids[r] / a.x_row_div : r;
-    return phys < 0 ? 0 : (phys >= a.x_rows ? a.x_rows - 1 : phys);
-  };
 
   // weights: as in the bf16 kernel (direct-to-LDS, chunk c of row r in slot c ^ (r % 8))
   __amdgpu_buffer_rsrc_t wrsrc[GROUPS];
@@ -459,6 +449,28 @@ __global__ __launch_bounds__(64 * WAVES, 1) void prefill_gemm_fp8_kernel(const G
     sreg[g] = lane < KB ? srow[lane] : 0.0f;
   }
   const int woff = (lane >> 3) * K + (((lane & 7) ^ (lane >> 3)) << 4);
+  uint8_t* const wring = lds + wave * WAVE_BLOCK;  // ring slot s at + s * 32 KB
+  // weight blocks 0 and 1 go out before the tile metadata, as in the bf16 kernel
+#pragma unroll
+  for (int blk = 0; blk < 2; ++blk)
+#pragma unroll
+    for (int g = 0; g < GROUPS; ++g)
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+        load_lds_16<kNonTemporal>(wrsrc[g], wring + blk * kStripeBlockBytes + (2 * g + h) * 1024,
+                                  blk < KB ? woff + 8 * h * K : kOutOfRange, blk < KB ? blk * kScaleBlock : 0);
+  const int r0 = uniform(a.tile_row[tile]);
+  const int live = uniform(a.tile_live[tile]);
+  if (uniform(a.tile_expert[tile]) != e || r0 < 0 || live <= 0 || live > kBM || r0 + live > a.rows) {
+    wait_all_loads();  // no load may still target LDS when the workgroup ends
+    return;
+  }
+  const int ncg = (live + 15) >> 4;
+  auto phys_row = [&](int row) -> int64_t {
+    const int r = r0 + (row < live ? row : 0);  // padding rows repeat a live row; their columns are dropped
+    int64_t phys = a.x_row_ids ? a.x_row_ids[r] / a.x_row_div : r;
+    return phys < 0 ? 0 : (phys >= a.x_rows ? a.x_rows - 1 : phys);
+  };
   const __amdgpu_buffer_rsrc_t xrsrc = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<uint8_t*>(a.xq), (short)0, (int)(a.x_rows * K), kBufferFormat);
   // activation block scales: waves 0 and 1 load tile rows 64 w + lane of each
@@ -477,6 +489,7 @@ __global__ __launch_bounds__(64 * WAVES, 1) void prefill_gemm_fp8_kernel(const G
     constexpr int XSTAGE = Rings::XSTAGE;
     static_assert(XSTAGE >= NCG * 16 * ROWB, "activation stage holds the tile's rows");
     static_assert(SW * kStripeBlockBytes + SX * (XSTAGE + SSTAGE) <= kPrefillLds, "LDS budget");
+    static_assert(SW >= 3, "weight blocks 0 and 1 are in flight before the variant is chosen");
     constexpr int PENDING = prefill_pending(SW, SX, XLOADS + 1, WLOADS);
     static_assert(PENDING >= 0 && PENDING < 64, "vmcnt range");
     f32x4 acc[TABLES][RG][NCG];
@@ -486,7 +499,6 @@ __global__ __launch_bounds__(64 * WAVES, 1) void prefill_gemm_fp8_kernel(const G
       for (int rg = 0; rg < RG; ++rg)
 #pragma unroll
         for (int cg = 0; cg < NCG; ++cg) acc[t][rg][cg] = f32x4{0.f, 0.f, 0.f, 0.f};
-    uint8_t* const wring = lds + wave * WAVE_BLOCK;
     uint8_t* const xring = lds + SW * kStripeBlockBytes;
     uint8_t* const sring = xring + SX * XSTAGE;
 
@@ -531,10 +543,13 @@ __global__ __launch_bounds__(64 * WAVES, 1) void prefill_gemm_fp8_kernel(const G
 #pragma unroll
     for (int i = -P; i < 0; ++i) {
       if (i + SX - 1 >= 0) issue_x(i + SX - 1);
-      if (i + SW - 1 >= 0) issue_w(i + SW - 1);
+      if (i + SW - 1 >= 2) issue_w(i + SW - 1);  // blocks 0 and 1 went out first
     }
     for (int kb = 0; kb < KB; ++kb) {
-      wait_loads_then_barrier<PENDING>();
+      if (kb == 0)
+        wait_loads_then_barrier<0>();  // block 0: every prologue load
+      else
+        wait_loads_then_barrier<PENDING>();
       issue_x(kb + SX - 1);
       issue_w(kb + SW - 1);
 
