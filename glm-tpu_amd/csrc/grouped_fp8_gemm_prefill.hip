@@ -82,6 +82,31 @@ __device__ __forceinline__ void wait_loads_then_barrier() {
 
 __device__ __forceinline__ void wait_all_loads() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
+// Output rows of the lane's route columns r0 + cg * 16 + lrow, as stored (the
+// epilogue checks them: out_row()).  The loads are unconditional (padding
+// columns read column 0's entry) and issued together; nothing uses them
+// before the epilogue, so nothing waits for them before it.
+template <int NCG>
+__device__ __forceinline__ void load_out_rows(const GroupedGemmArgs& a, int r0, int live, int lrow, int (&orow)[NCG]) {
+  int r[NCG];
+#pragma unroll
+  for (int cg = 0; cg < NCG; ++cg) r[cg] = r0 + (cg * 16 + lrow < live ? cg * 16 + lrow : 0);
+  if (a.out_row_ids != nullptr) {
+#pragma unroll
+    for (int cg = 0; cg < NCG; ++cg) orow[cg] = a.out_row_ids[r[cg]];
+  } else {
+#pragma unroll
+    for (int cg = 0; cg < NCG; ++cg) orow[cg] = r[cg];
+  }
+}
+
+// The output row of column `col` given load_out_rows' entry, or -1 (padding
+// column, or a row outside the output).
+__device__ __forceinline__ int64_t out_row(const GroupedGemmArgs& a, int col, int live, int stored) {
+  return col < live && stored >= 0 && stored < a.out_rows ? stored : -1;
+}
+
+
 // 16 bytes a lane from rsrc + voffset + soffset straight into LDS at
 // lds + 16 * lane (buffer_load_dwordx4 ... lds).  The builtin only exists for
 // the device target; the host pass of the kernel template must not see it.
@@ -259,11 +284,7 @@ __global__ __launch_bounds__(64 * WAVES, 1) void prefill_gemm_kernel(const Group
     // output rows of this lane's route columns, loaded ahead of the streams so
     // the epilogue waits at most for the weighted epilogue's route weights
     int orow[NCG];
-#pragma unroll
-    for (int cg = 0; cg < NCG; ++cg) {
-      const int col = cg * 16 + lrow;
-      orow[cg] = col < live ? (int)fragment_row(a, r0 + col) : -1;
-    }
+    load_out_rows(a, r0, live, lrow, orow);
 
     // prologue: the issue schedule's iterations -P .. -1
     constexpr int P = (SX > SW ? SX : SW) - 1;
@@ -344,14 +365,17 @@ __global__ __launch_bounds__(64 * WAVES, 1) void prefill_gemm_kernel(const Group
     wait_all_loads();  // no load may still target LDS when the workgroup ends
 
     // Epilogue: lane holds rows n .. n+3 of route column cg*16 + lrow.
+    int64_t orow_ok[NCG];
+#pragma unroll
+    for (int cg = 0; cg < NCG; ++cg) orow_ok[cg] = out_row(a, cg * 16 + lrow, live, orow[cg]);
     float wgt[NCG];  // every route weight load in flight at once
 #pragma unroll
-    for (int cg = 0; cg < NCG; ++cg) wgt[cg] = fragment_weight<EPI>(a, orow[cg]);
+    for (int cg = 0; cg < NCG; ++cg) wgt[cg] = fragment_weight<EPI>(a, orow_ok[cg]);
 #pragma unroll
     for (int cg = 0; cg < NCG; ++cg)
 #pragma unroll
       for (int rg = 0; rg < RG; ++rg)
-        store_fragment_at<TABLES, EPI>(a, orow[cg], wgt[cg], n0 + rg * 16 + lgrp * 4, acc[0][rg][cg],
+        store_fragment_at<TABLES, EPI>(a, orow_ok[cg], wgt[cg], n0 + rg * 16 + lgrp * 4, acc[0][rg][cg],
                                        acc[TABLES - 1][rg][cg]);
   };
   switch (ncg) {
@@ -534,11 +558,7 @@ __global__ __launch_bounds__(64 * WAVES, 1) void prefill_gemm_fp8_kernel(const G
     };
 
     int orow[NCG];  // as in the bf16 kernel: output rows loaded ahead of the streams
-#pragma unroll
-    for (int cg = 0; cg < NCG; ++cg) {
-      const int col = cg * 16 + lrow;
-      orow[cg] = col < live ? (int)fragment_row(a, r0 + col) : -1;
-    }
+    load_out_rows(a, r0, live, lrow, orow);
     constexpr int P = (SX > SW ? SX : SW) - 1;
 #pragma unroll
     for (int i = -P; i < 0; ++i) {
@@ -587,14 +607,17 @@ __global__ __launch_bounds__(64 * WAVES, 1) void prefill_gemm_fp8_kernel(const G
       }
     }
     wait_all_loads();
+    int64_t orow_ok[NCG];
+#pragma unroll
+    for (int cg = 0; cg < NCG; ++cg) orow_ok[cg] = out_row(a, cg * 16 + lrow, live, orow[cg]);
     float wgt[NCG];  // every route weight load in flight at once
 #pragma unroll
-    for (int cg = 0; cg < NCG; ++cg) wgt[cg] = fragment_weight<EPI>(a, orow[cg]);
+    for (int cg = 0; cg < NCG; ++cg) wgt[cg] = fragment_weight<EPI>(a, orow_ok[cg]);
 #pragma unroll
     for (int cg = 0; cg < NCG; ++cg)
 #pragma unroll
       for (int rg = 0; rg < RG; ++rg)
-        store_fragment_at<TABLES, EPI>(a, orow[cg], wgt[cg], n0 + rg * 16 + lgrp * 4, acc[0][rg][cg],
+        store_fragment_at<TABLES, EPI>(a, orow_ok[cg], wgt[cg], n0 + rg * 16 + lgrp * 4, acc[0][rg][cg],
                                        acc[TABLES - 1][rg][cg]);
   };
   switch (ncg) {
