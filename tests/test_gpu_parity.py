@@ -443,6 +443,8 @@ def _small_case(tokens, experts, hidden, inter, top_k, zipf, seed):
     (512, 16, 512, 256, 8, 1.2),    # wide path, skewed: multi-tile experts
     (300, 64, 256, 512, 6, 0.0),    # wide path, ragged tiles
     (64, 4, 8448, 256, 2, 0.0),     # K/128 = 66 > 64: the 64-bit-offset wide kernel instead of the prefill one
+    (512, 256, 768, 256, 8, 0.0),   # prefill path over 256 experts of ~16 routes (one tile each)
+    (1536, 256, 768, 256, 8, 1.2),  # 256 experts, skewed: single- and multi-tile experts side by side
 ])
 def test_routed_experts_matches_oracle(device, tokens, experts, hidden, inter, top_k, zipf):
     from glm_moe.layers.moe.routed_experts import routed_experts
