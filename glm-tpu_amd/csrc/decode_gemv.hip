@@ -43,6 +43,7 @@ constexpr int kStepK = 256;        // K per step: 16 lanes x 16 e4m3 bytes
 constexpr int kMaxWaveSteps = 8;   // K range of one wave: 2048 (LDS staging, lane-held scales)
 constexpr int kGateUpWaves = 4;
 constexpr int kDownWaves = 8;
+constexpr int kDownWavesFew = 4;   // <= 8 routes, no shared expert: 3 four-wave workgroups per CU, one pass
 constexpr int kGateUpDepth = 2;    // two tables: 2 x 32 VGPRs in flight
 constexpr int kDownRows = 8;       // down: weight rows per workgroup (H / 8 = 768 workgroups: 3 per CU)
 constexpr int kDownQuads = kDownRows / 4;
@@ -644,13 +645,21 @@ hipError_t launch_decode_routed(const DecodeArgs& a, hipStream_t stream, const L
                                  a, gu_steps);
   if (err != hipSuccess) return err;
   const int d_steps = (a.intermediate + kStepK - 1) / kStepK;
+  // Eight-wave workgroups (one route per wave) for many routes or the resident
+  // shared expert; for a single token's routes four-wave workgroups of two
+  // routes a wave, which all fit on the GPU at once (768 x 4 waves).
+  const bool few = !resident && a.routes <= 2 * kDownWavesFew;
+  const int d_waves = few ? kDownWavesFew : kDownWaves;
   const size_t d_lds = sizeof(float) * kMaxDecodeRoutes * kGemvRows +
-                       sizeof(uint16_t) * kDownWaves * xs_elems(d_steps) +
+                       sizeof(uint16_t) * d_waves * xs_elems(d_steps) +
                        (resident ? sizeof(float) * kMaxDecodeRoutes * kGemvRows : 0);
   if (stage_events) next_launch_events() = stage_events[1];
   if (resident)
     return launch_kernel(decode_down_kernel<kDownWaves, true>, dim3(a.hidden / kDownRows), dim3(64 * kDownWaves),
                          d_lds, stream, a);
+  if (few)
+    return launch_kernel(decode_down_kernel<kDownWavesFew, false>, dim3(a.hidden / kDownRows),
+                         dim3(64 * kDownWavesFew), d_lds, stream, a);
   return launch_kernel(decode_down_kernel<kDownWaves, false>, dim3(a.hidden / kDownRows), dim3(64 * kDownWaves),
                        d_lds, stream, a);
 }
