@@ -220,7 +220,8 @@ def full_layer(work, steps, warmup):
     Returns (us per layer, algorithmic bytes of the shared expert, how)."""
     import torch
 
-    from glm_moe.layers.moe.routed_experts import _shared_swiglu, routed_experts, uses_decode_kernels
+    from glm_moe.layers.moe.routed_experts import (_shared_expert, routed_experts, shared_expert_rows_fit,
+                                                   uses_decode_kernels)
 
     cfg = work.cfg
     device = work.inputs[0][0].device
@@ -244,7 +245,7 @@ def full_layer(work, steps, warmup):
         if resident:
             routed_experts(x, ids, w, *tables, out=out, shared_tables=(sg, su, sd), routed_scale=2.5)
         else:
-            shared = _shared_swiglu(x, sg, su, sd)
+            shared = _shared_expert(x, sg, su, sd)
             routed_experts(x, ids, w, *tables, out=out, shared=shared, routed_scale=2.5,
                            activations=work.activations)
 
@@ -266,8 +267,12 @@ def full_layer(work, steps, warmup):
     torch.cuda.synchronize()
     del graph
     shared_bytes = 3 * inter_shared * cfg.hidden * 2
-    how = ("shared expert inside the two decode kernels (glm_moe_moe_layer_resident)" if resident else
-           "shared expert on torch/hipBLASLt, epilogue fused (glm_moe_moe_layer)")
+    if resident:
+        how = "shared expert inside the two decode kernels (glm_moe_moe_layer_resident)"
+    elif shared_expert_rows_fit(cfg.tokens, cfg.hidden, inter_shared):
+        how = "shared expert on the few-row kernels (glm_moe_shared_expert_rows), epilogue fused (glm_moe_moe_layer)"
+    else:
+        how = "shared expert on torch/hipBLASLt, epilogue fused (glm_moe_moe_layer)"
     return start.elapsed_time(stop) / steps * 1e3, shared_bytes, how
 
 

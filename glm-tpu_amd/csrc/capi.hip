@@ -736,6 +736,30 @@ int glm_moe_moe_layer_from_logits(const uint16_t* hidden, int64_t tokens, int64_
                              valid, workspace, workspace_bytes, StageTimer{nullptr, nullptr}, stream, &router);
 }
 
+size_t glm_moe_shared_expert_rows_workspace_bytes(int64_t tokens, int64_t shared_intermediate) {
+  if (tokens <= 0 || shared_intermediate <= 0) return 0;
+  return (size_t)tokens * (size_t)shared_intermediate * sizeof(uint16_t);
+}
+
+int glm_moe_shared_expert_rows(const uint16_t* hidden, int64_t tokens, int64_t hidden_size,
+                               const uint16_t* shared_gate, const uint16_t* shared_up, const uint16_t* shared_down,
+                               int64_t shared_intermediate, uint16_t* out, void* workspace, size_t workspace_bytes,
+                               void* stream) {
+  GLM_REQUIRE(hidden && shared_gate && shared_up && shared_down && out, "null tensor pointer");
+  GLM_REQUIRE(shared_rows_fit(tokens, hidden_size, shared_intermediate),
+              "the few-row shared expert takes 1 to %d rows and hidden / intermediate sizes that are multiples "
+              "of 128 (at most 8192 for 8 rows)",
+              kSharedRowsMax);
+  const size_t need = glm_moe_shared_expert_rows_workspace_bytes(tokens, shared_intermediate);
+  if (workspace == nullptr || workspace_bytes < need)
+    return fail(GLM_MOE_ERR_WORKSPACE, "workspace of %zu bytes needed, %zu given", need, workspace_bytes);
+  GLM_HIP(launch_shared_expert_rows(hidden, (int)tokens, (int)hidden_size, (int)shared_intermediate, shared_gate,
+                                    shared_up, shared_down, static_cast<uint16_t*>(workspace), out,
+                                    as_stream(stream)),
+          "shared expert launch");
+  return GLM_MOE_OK;
+}
+
 int glm_moe_event_create(void** event) {
   GLM_REQUIRE(event != nullptr, "null event slot");
   hipEvent_t e = nullptr;

@@ -609,6 +609,148 @@ void decode_down_kernel(const DecodeArgs a) {
   }
 }
 
+
+// ------------------------------------------------------------------ bf16 shared expert over a few rows
+// For tokens > 1 the resident path above streams the shared tables once per
+// token; these two kernels stream them once for all NT rows.  Workgroup = 8
+// weight rows (two quads) x every row; its 4 waves split K; a wave stages its
+// K range of all NT activation rows in its LDS region and, per step of 128 K,
+// multiplies the 8 weight rows' bf16 chunks (4 rows x 256 B per load, as the
+// resident path) with each row's chunk in v_dot2c_f32_bf16 (exact products,
+// FP32 sums).  Rounding points as the resident path: bf16 gate and up sums,
+// bf16 SwiGLU, bf16 down sums.
+constexpr int kSharedWgRows = 8;
+constexpr int kSharedWaves = 4;
+constexpr int kSharedQuads = kSharedWgRows / 4;
+
+template <int TABLES, int NT>
+__device__ __forceinline__ void bf16_rows_fma(const u32x4 (&w)[TABLES][kSharedQuads], const uint16_t* xs, int range,
+                                              int s, int lane, float (&acc)[TABLES][kSharedQuads][NT]) {
+#pragma unroll
+  for (int t = 0; t < NT; ++t) {
+    const u32x4 x = *reinterpret_cast<const u32x4*>(xs + t * range + s * kBf16StepK + (lane & 15) * 8);
+#pragma unroll
+    for (int tb = 0; tb < TABLES; ++tb)
+#pragma unroll
+      for (int q = 0; q < kSharedQuads; ++q) {
+        float a = acc[tb][q][t];
+#pragma unroll
+        for (int h = 0; h < 4; ++h) {
+          const uint32_t wv = w[tb][q][h], xv = x[h];
+          a = __builtin_amdgcn_fdot2_f32_bf16(as_bf16x2(wv), as_bf16x2(xv), a, false);
+        }
+        acc[tb][q][t] = a;
+      }
+  }
+}
+
+// One wave: K range [step_begin, step_end) of the 8 rows of every table against
+// NT rows x[t * k + ...], staged at xs (NT x range elements).
+template <int TABLES, int NT>
+__device__ __forceinline__ void bf16_rows_run(Bf16Stream<TABLES>& g, const uint16_t* x, int range, int lane,
+                                              float (&acc)[TABLES][kSharedQuads][NT]) {
+  const int n = g.step_end - g.step_begin;
+  if (n <= 0) return;
+  const int last = n - 1;
+  const int kbeg = g.step_begin * kBf16StepK;
+  const int per_row = (n * kBf16StepK) >> 3;  // 16-byte chunks of one row's range
+  for (int c = lane; c < NT * per_row; c += 64) {
+    const int t = c / per_row, i = c % per_row;
+    *reinterpret_cast<u32x4*>(g.xs + t * range + 8 * i) =
+        *reinterpret_cast<const u32x4*>(x + (int64_t)t * g.k + kbeg + 8 * i);
+  }
+  constexpr int D = 2;
+  u32x4 ring[D][TABLES][kSharedQuads];
+#pragma unroll
+  for (int d = 0; d < D; ++d) {
+    bf16_load(g, min(d, last), ring[d]);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  for (int s = 0; s < n; s += D) {
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+      if (s + d < n) bf16_rows_fma<TABLES, NT>(ring[d], g.xs, range, s + d, lane, acc);
+      __builtin_amdgcn_sched_barrier(0);
+      bf16_load(g, min(s + d + D, last), ring[d]);
+    }
+  }
+}
+
+__host__ __device__ constexpr int shared_wave_steps(int k) { return ((k / kBf16StepK) + kSharedWaves - 1) / kSharedWaves; }
+
+// TABLES == 2: gate/up rows of `intermediate`, SwiGLU into act [NT, I].
+// TABLES == 1: down rows of `hidden` from act, into out [NT, H].
+template <int TABLES, int NT>
+__global__ __launch_bounds__(64 * kSharedWaves) void shared_rows_kernel(const uint16_t* x, int k,
+                                                                         const uint16_t* w0, const uint16_t* w1,
+                                                                         int n, uint16_t* out) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  float(*red)[TABLES][kSharedWgRows][NT] = reinterpret_cast<float(*)[TABLES][kSharedWgRows][NT]>(smem);
+  const int lane = threadIdx.x & 63;
+  const int wave = uniform(threadIdx.x >> 6);
+  const int row0 = blockIdx.x * kSharedWgRows;
+  const int ws = shared_wave_steps(k);
+  const int range = ws * kBf16StepK;
+  Bf16Stream<TABLES> g;
+  g.k = k;
+  g.row_bytes = 2 * k;
+  g.lane_off = (uint32_t)((lane >> 4) * 2 * k + (lane & 15) * 16);
+  g.step_begin = min(wave * ws, k / kBf16StepK);
+  g.step_end = min(g.step_begin + ws, k / kBf16StepK);
+  const uint16_t* tables[2] = {w0, w1};
+#pragma unroll
+  for (int tb = 0; tb < TABLES; ++tb)
+    g.w[tb] = rows_buffer(reinterpret_cast<const uint8_t*>(tables[tb] + (int64_t)row0 * k),
+                          (int64_t)kSharedWgRows * 2 * k);
+  g.x = nullptr;
+  g.xs = reinterpret_cast<uint16_t*>(smem + sizeof(float) * kSharedWaves * TABLES * kSharedWgRows * NT) +
+         wave * NT * range;
+  float acc[TABLES][kSharedQuads][NT] = {};
+  bf16_rows_run<TABLES, NT>(g, x, range, lane, acc);
+#pragma unroll
+  for (int tb = 0; tb < TABLES; ++tb)
+#pragma unroll
+    for (int q = 0; q < kSharedQuads; ++q)
+#pragma unroll
+      for (int t = 0; t < NT; ++t) {
+        const float v = sum16(acc[tb][q][t]);
+        if ((lane & 15) == 0) red[wave][tb][4 * q + (lane >> 4)][t] = v;
+      }
+  __syncthreads();
+  const int tid = threadIdx.x;
+  if (tid < kSharedWgRows * NT) {
+    const int row = tid % kSharedWgRows, t = tid / kSharedWgRows;
+    float s0 = 0.f, s1 = 0.f;
+    for (int w = 0; w < kSharedWaves; ++w) {  // wave order: deterministic
+      s0 += red[w][0][row][t];
+      s1 += red[w][TABLES - 1][row][t];
+    }
+    const float v = TABLES == 2 ? swiglu_bf16(round_to_bf16(s0), round_to_bf16(s1)) : s0;
+    out[(int64_t)t * n + row0 + row] = f32_to_bf16_bits(v);
+  }
+}
+
+template <int TABLES, int NT>
+hipError_t launch_shared_rows(const uint16_t* x, int k, const uint16_t* w0, const uint16_t* w1, int n, uint16_t* out,
+                              hipStream_t stream) {
+  static std::atomic<uint64_t> lds_set{0};
+  const hipError_t err = allow_full_lds(reinterpret_cast<const void*>(shared_rows_kernel<TABLES, NT>), lds_set);
+  if (err != hipSuccess) return err;
+  const size_t lds = sizeof(float) * kSharedWaves * TABLES * kSharedWgRows * NT +
+                     sizeof(uint16_t) * kSharedWaves * NT * shared_wave_steps(k) * kBf16StepK;
+  return launch_kernel(shared_rows_kernel<TABLES, NT>, dim3(n / kSharedWgRows), dim3(64 * kSharedWaves), lds, stream,
+                       x, k, w0, w1, n, out);
+}
+
+template <int NT>
+hipError_t launch_shared_expert_nt(const uint16_t* x, int hidden, int intermediate, const uint16_t* gate,
+                                   const uint16_t* up, const uint16_t* down, uint16_t* act, uint16_t* out,
+                                   hipStream_t stream) {
+  hipError_t err = launch_shared_rows<2, NT>(x, hidden, gate, up, intermediate, act, stream);
+  if (err != hipSuccess) return err;
+  return launch_shared_rows<1, NT>(act, intermediate, down, nullptr, hidden, out, stream);
+}
+
 int gate_up_wave_steps(int hidden) {
   const int steps = (hidden + kStepK - 1) / kStepK;
   return (steps + kGateUpWaves - 1) / kGateUpWaves;
@@ -619,6 +761,34 @@ int gate_up_wave_steps(int hidden) {
 bool decode_path_fits(int64_t hidden, int64_t intermediate) {
   return hidden % kGemvRows == 0 && hidden <= (int64_t)kGateUpWaves * kMaxWaveSteps * kStepK &&
          intermediate <= (int64_t)kMaxWaveSteps * kStepK;
+}
+
+// The staged rows of a wave (NT x its K range, bf16) must fit in LDS next to
+// the sums; weight rows come in workgroups of 8 and K in steps of 128.
+bool shared_rows_fit(int64_t tokens, int64_t hidden, int64_t intermediate) {
+  if (tokens < 1 || tokens > kSharedRowsMax || hidden <= 0 || intermediate <= 0) return false;
+  if (hidden % kScaleBlock != 0 || intermediate % kScaleBlock != 0) return false;
+  if (hidden > (1 << 20) || intermediate > (1 << 20)) return false;
+  const int64_t kmax = hidden > intermediate ? hidden : intermediate;
+  const int64_t lds = (int64_t)sizeof(float) * kSharedWaves * 2 * kSharedWgRows * tokens +
+                      2 * kSharedWaves * tokens * (int64_t)shared_wave_steps((int)kmax) * kBf16StepK;
+  return lds <= 160 * 1024;
+}
+
+hipError_t launch_shared_expert_rows(const uint16_t* x, int tokens, int hidden, int intermediate,
+                                     const uint16_t* gate, const uint16_t* up, const uint16_t* down,
+                                     uint16_t* act, uint16_t* out, hipStream_t stream) {
+  if (!shared_rows_fit(tokens, hidden, intermediate)) return hipErrorInvalidValue;
+  switch (tokens) {
+    case 1: return launch_shared_expert_nt<1>(x, hidden, intermediate, gate, up, down, act, out, stream);
+    case 2: return launch_shared_expert_nt<2>(x, hidden, intermediate, gate, up, down, act, out, stream);
+    case 3: return launch_shared_expert_nt<3>(x, hidden, intermediate, gate, up, down, act, out, stream);
+    case 4: return launch_shared_expert_nt<4>(x, hidden, intermediate, gate, up, down, act, out, stream);
+    case 5: return launch_shared_expert_nt<5>(x, hidden, intermediate, gate, up, down, act, out, stream);
+    case 6: return launch_shared_expert_nt<6>(x, hidden, intermediate, gate, up, down, act, out, stream);
+    case 7: return launch_shared_expert_nt<7>(x, hidden, intermediate, gate, up, down, act, out, stream);
+    default: return launch_shared_expert_nt<8>(x, hidden, intermediate, gate, up, down, act, out, stream);
+  }
 }
 
 hipError_t launch_decode_routed(const DecodeArgs& a, hipStream_t stream, const LaunchEvents* stage_events) {

@@ -632,20 +632,6 @@ __global__ __launch_bounds__(64 * WAVES, 1) void prefill_gemm_fp8_kernel(const G
   }
 }
 
-// Lets `kernel` use the whole 160 KB of LDS on the current device.  `done` is
-// the caller's per-kernel mask of devices already set (the attribute is
-// per device; setting it twice is harmless, so racing threads are fine).
-inline hipError_t allow_full_lds(const void* kernel, std::atomic<uint64_t>& done) {
-  int dev = 0;
-  hipError_t err = hipGetDevice(&dev);
-  if (err != hipSuccess) return err;
-  const uint64_t bit = dev < 64 ? (1ull << dev) : 0;
-  if (bit != 0 && (done.load(std::memory_order_acquire) & bit)) return hipSuccess;
-  err = hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, kPrefillLds);
-  if (err == hipSuccess) done.fetch_or(bit, std::memory_order_release);
-  return err;
-}
-
 template <int TABLES, int RG, int WAVES, int EPI>
 hipError_t launch_prefill_fp8(const GroupedGemmArgs& a, hipStream_t stream) {
   constexpr int BN = WAVES * RG * 16;

@@ -5,9 +5,24 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <atomic>
 #include <utility>
 
 namespace glm_moe {
+
+// Lets `kernel` use the whole 160 KB of LDS of a CU on the current device.
+// `done` is the caller's per-kernel mask of devices already set (the attribute
+// is per device; setting it twice is harmless, so racing threads are fine).
+inline hipError_t allow_full_lds(const void* kernel, std::atomic<uint64_t>& done) {
+  int dev = 0;
+  hipError_t err = hipGetDevice(&dev);
+  if (err != hipSuccess) return err;
+  const uint64_t bit = dev < 64 ? (1ull << dev) : 0;
+  if (bit != 0 && (done.load(std::memory_order_acquire) & bit)) return hipSuccess;
+  err = hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+  if (err == hipSuccess) done.fetch_or(bit, std::memory_order_release);
+  return err;
+}
 
 // ------------------------------------------------------------------ launches
 // Stage timing: a caller may arm a (start, stop) pair of HIP events for the
@@ -203,6 +218,15 @@ constexpr int kDecodeRouterExperts = 256;
 bool decode_path_fits(int64_t hidden, int64_t intermediate);
 // stage_events: null, or the armed events of the gate/up [0] and down [1] kernels.
 hipError_t launch_decode_routed(const DecodeArgs& a, hipStream_t stream, const LaunchEvents* stage_events);
+
+// The bf16 shared expert over a few rows (tokens <= kSharedRowsMax): gate/up
+// [I, H], SwiGLU and down [H, I] with the resident path's rounding points,
+// every weight byte read once for all rows.  act: workspace [tokens, I] bf16.
+constexpr int kSharedRowsMax = 8;
+bool shared_rows_fit(int64_t tokens, int64_t hidden, int64_t intermediate);
+hipError_t launch_shared_expert_rows(const uint16_t* x, int tokens, int hidden, int intermediate,
+                                     const uint16_t* gate, const uint16_t* up, const uint16_t* down,
+                                     uint16_t* act, uint16_t* out, hipStream_t stream);
 
 // ------------------------------------------------------------------ auxiliary
 hipError_t launch_decode_fp8_table(const uint8_t* bits, const float* scale, int64_t n, int64_t k,

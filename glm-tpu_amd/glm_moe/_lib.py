@@ -79,6 +79,8 @@ SIGNATURES: dict[str, tuple] = {
         [_vp, _i64, _i64, _vp, _vp, _i32, _i32, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _u32, _vp, _vp, _vp, _i64, _f,
          _vp, _vp, _vp, _vp, _vp, _sz, _vp],
     ),
+    "glm_moe_shared_expert_rows_workspace_bytes": (_sz, [_i64, _i64]),
+    "glm_moe_shared_expert_rows": (ctypes.c_int, [_vp, _i64, _i64, _vp, _vp, _vp, _i64, _vp, _vp, _sz, _vp]),
     "glm_moe_event_create": (ctypes.c_int, [ctypes.POINTER(_vp)]),
     "glm_moe_event_destroy": (ctypes.c_int, [_vp]),
     "glm_moe_event_elapsed_ms": (ctypes.c_int, [_vp, _vp, ctypes.POINTER(_f)]),

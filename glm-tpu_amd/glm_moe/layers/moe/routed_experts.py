@@ -313,6 +313,49 @@ def _shared_swiglu(hidden: torch.Tensor, gate: torch.Tensor, up: torch.Tensor, d
     return act @ down.t()
 
 
+SHARED_ROWS_MAX = 8  # rows the few-row shared-expert kernels take (glm_moe_shared_expert_rows)
+
+
+def shared_expert_rows_fit(tokens: int, hidden: int, intermediate: int) -> bool:
+    """Whether glm_moe_shared_expert_rows takes this geometry (1..8 rows, sizes
+    multiples of 128 and at most 8192)."""
+    return (1 <= tokens <= SHARED_ROWS_MAX and hidden % 128 == 0 and intermediate % 128 == 0
+            and 0 < hidden <= 8192 and 0 < intermediate <= 8192)
+
+
+def shared_expert_rows(hidden: torch.Tensor, gate: torch.Tensor, up: torch.Tensor,
+                       down: torch.Tensor) -> torch.Tensor:
+    """The bf16 shared expert of a few rows on the library's kernels: ``bf16 [T, H]``.
+
+    Same rounding points as ``_shared_swiglu`` (``routed_experts.py:119-124`` /
+    ``:269-302``), with every weight byte read once for all ``T <= 8`` rows in
+    two launches instead of three GEMMs and the elementwise SwiGLU.
+    """
+    tokens, h = hidden.shape
+    inter = gate.shape[0]
+    if not shared_expert_rows_fit(tokens, h, inter):
+        raise ValueError("the few-row shared expert takes 1..8 rows and sizes that are multiples of 128, <= 8192")
+    if (tuple(gate.shape) != (inter, h) or tuple(up.shape) != (inter, h) or tuple(down.shape) != (h, inter)
+            or any(t.dtype != torch.bfloat16 for t in (hidden, gate, up, down))):
+        raise ValueError("shared expert tables must be bf16 [I, H], [I, H], [H, I] for bf16 [T, H] rows")
+    x, g, u, d = (t.contiguous() for t in (hidden, gate, up, down))
+    _lib.require_device(x, g, u, d)
+    out = torch.empty((tokens, h), dtype=torch.bfloat16, device=x.device)
+    ws = torch.empty(int(_lib.lib().glm_moe_shared_expert_rows_workspace_bytes(tokens, inter)),
+                     dtype=torch.uint8, device=x.device)
+    _lib.call("glm_moe_shared_expert_rows", _lib.ptr(x), tokens, h, _lib.ptr(g), _lib.ptr(u), _lib.ptr(d), inter,
+              _lib.ptr(out), _lib.ptr(ws), ws.numel(), _lib.stream_of(x))
+    return out
+
+
+def _shared_expert(hidden: torch.Tensor, gate: torch.Tensor, up: torch.Tensor, down: torch.Tensor) -> torch.Tensor:
+    """The shared expert's bf16 output rows: the few-row kernels for up to 8
+    rows, torch GEMMs on hipBLASLt (which read the weights once per call) above."""
+    if shared_expert_rows_fit(hidden.shape[0], hidden.shape[1], gate.shape[0]):
+        return shared_expert_rows(hidden, gate, up, down)
+    return _shared_swiglu(hidden, gate, up, down)
+
+
 def _check_layer_shapes(hidden_local, route_indices, route_weights, gate_bits, up_bits, down_bits,
                         contract: GlmMoeNumericalContract, *, rows_exact: int | None) -> None:
     if contract.stage_size != 1:
@@ -374,10 +417,10 @@ def prefill_moe_from_routes(
     tables = (shared_gate_local, shared_up_local, shared_down_local)
     if hidden_local.shape[0] == 1 and uses_decode_kernels(1, contract.top_k, h, inter):
         # one row: the shared expert runs inside the two decode kernels (with more
-        # rows they would stream its weights once per row; hipBLASLt reads them once)
+        # rows they would stream its weights once per row)
         shared_kw = {"shared_tables": tuple(t.contiguous() for t in tables)}
     else:
-        shared_kw = {"shared": _shared_swiglu(hidden_local, *tables)}
+        shared_kw = {"shared": _shared_expert(hidden_local, *tables)}
     return routed_experts(
         hidden_local, route_indices, route_weights, expert_gate_bits_local, expert_gate_scale_local,
         expert_up_bits_local, expert_up_scale_local, expert_down_bits_local, expert_down_scale_local,
@@ -425,7 +468,7 @@ def moe_grouped_routes(
     if uses_decode_kernels(1, contract.top_k, h, inter):
         shared_kw = {"shared_tables": tuple(t.contiguous() for t in shared_bf16)}
     else:
-        shared_kw = {"shared": _shared_swiglu(hidden_local, *shared_bf16)}
+        shared_kw = {"shared": _shared_expert(hidden_local, *shared_bf16)}
     output, _ = routed_experts(
         hidden_local, route_indices, route_weights, expert_gate_bits_local, expert_gate_scale_local,
         expert_up_bits_local, expert_up_scale_local, expert_down_bits_local, expert_down_scale_local,

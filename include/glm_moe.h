@@ -250,6 +250,22 @@ int glm_moe_moe_layer_from_logits(const uint16_t* hidden, int64_t tokens, int64_
                                   int32_t* route_indices, float* route_weights, uint16_t* out, uint8_t* valid,
                                   void* workspace, size_t workspace_bytes, void* stream);
 
+/* The bf16 shared expert of a few rows (1 <= tokens <= 8): gate and up
+ * [shared_intermediate, hidden_size], SwiGLU, down [hidden_size,
+ * shared_intermediate], out [tokens, hidden_size] bf16, in two launches that
+ * read every weight byte once for all rows.  Replaces the resident bf16 shared
+ * expert of the layer bodies (glm_tpu/layers/moe/routed_experts.py:119-124 and
+ * :269-302; resident_matmul, glm_tpu/layers/linear.py:26-33) at their
+ * rounding points: bf16 gate and up sums, bf16 SwiGLU (:123, :280), bf16 down
+ * sums; FP32 accumulation of exact bf16 products.  Its output is the `shared`
+ * input of glm_moe_moe_layer.  Workspace: the SwiGLU rows,
+ * glm_moe_shared_expert_rows_workspace_bytes(tokens, shared_intermediate). */
+size_t glm_moe_shared_expert_rows_workspace_bytes(int64_t tokens, int64_t shared_intermediate);
+int glm_moe_shared_expert_rows(const uint16_t* hidden, int64_t tokens, int64_t hidden_size,
+                               const uint16_t* shared_gate, const uint16_t* shared_up, const uint16_t* shared_down,
+                               int64_t shared_intermediate, uint16_t* out, void* workspace, size_t workspace_bytes,
+                               void* stream);
+
 /* Synthetic FP8 expert tables for tests and benchmarks, the reference's fixture
  * recipe (tools/equivalence/fixture.py:158-172) with 128x128 block scales:
  * w ~ N(0, sigma) (counter-based hash + Box-Muller), scale = amax/448 per block,

@@ -754,3 +754,48 @@ def test_layer_from_router_logits_known_answers_and_python_api(device):
     np.testing.assert_array_equal(ids.cpu().numpy(), ref_ids.cpu().numpy())
     ref = moe_grouped_routes(x_dev, ref_ids, ref_w, *tabs, contract=contract, shared_bf16=tuple(shared_dev))
     np.testing.assert_array_equal(bf16_bits_of(update), bf16_bits_of(ref))
+
+
+# ----------------------------------------------------------------------------- few-row shared expert
+@pytest.mark.parametrize("tokens,hidden,inter", [(1, 512, 256), (2, 768, 384), (4, 6144, 2048), (8, 1024, 512)])
+def test_shared_expert_rows_matches_oracle(device, tokens, hidden, inter):
+    """glm_moe_shared_expert_rows against the oracle's shared expert
+    (routed_experts.py:119-124 rounding points) and against the torch/hipBLASLt
+    GEMMs it replaces (equal up to FP32 summation order)."""
+    from glm_moe.layers.moe.routed_experts import _shared_swiglu, shared_expert_rows
+
+    rng = np.random.default_rng(tokens * 7 + hidden)
+    x = rng.standard_normal((tokens, hidden)).astype(np.float32)
+    tables = [(rng.standard_normal(shape) * std).astype(np.float32)
+              for shape, std in (((inter, hidden), hidden ** -0.5), ((inter, hidden), hidden ** -0.5),
+                                 ((hidden, inter), 2 * inter ** -0.5))]
+    x16 = O.bf16_round(x)
+    t16 = [O.bf16_round(t) for t in tables]
+    got = shared_expert_rows(bf16_dev(x16, device), *(bf16_dev(t, device) for t in t16))
+    ref = O.shared_expert(x16, *t16)
+    print("vs oracle:", assert_moe_close(host_f32(got), ref))
+    other = _shared_swiglu(bf16_dev(x16, device), *(bf16_dev(t, device) for t in t16))
+    print("vs hipBLASLt:", assert_moe_close(host_f32(got), host_f32(other)))
+    again = shared_expert_rows(bf16_dev(x16, device), *(bf16_dev(t, device) for t in t16))
+    np.testing.assert_array_equal(bf16_bits_of(again), bf16_bits_of(got))
+
+
+def test_prefill_layer_few_rows_uses_the_shared_rows_kernels(device, golden):
+    """prefill_moe_from_routes on 4 toy rows (few-row shared expert kernels) equals
+    the golden layer within tolerance and the same layer with the torch shared expert."""
+    from glm_moe.contracts import single_gpu_contract
+    from glm_moe.layers.moe.routed_experts import _shared_swiglu, prefill_moe_from_routes, routed_experts
+
+    g = golden
+    contract = single_gpu_contract(hidden_size=256, intermediate_size=256, num_experts=8, top_k=2)
+    x = dev(g["hidden_bits"].view(np.int16), device).view(torch.bfloat16)
+    ids, w = dev(g["route_indices"], device), dev(g["route_weights"], device)
+    t = _device_tables(g, device)
+    shared = [dev(g[k].view(np.int16), device).view(torch.bfloat16)
+              for k in ("shared_gate_bits", "shared_up_bits", "shared_down_bits")]
+    out, ok = prefill_moe_from_routes(x, ids, w, *(t[k] for k in TABLE_KEYS), *shared, contract=contract)
+    assert bool(ok)
+    print("toy layer, few-row shared expert:", assert_moe_close(host_f32(out), O.bf16_from_bits(g["layer_bits"])))
+    other, _ = routed_experts(x, ids, w, *(t[k] for k in TABLE_KEYS), shared=_shared_swiglu(x, *shared),
+                              routed_scale=2.5, check_weights=True)
+    print("vs torch shared expert:", assert_moe_close(host_f32(out), host_f32(other)))

@@ -131,6 +131,17 @@ def test_static_refusals_raise_value_error_through_the_abi():
         _lib.check(from_logits(1, 512, fake, fake))
     with pytest.raises(ValueError, match="decode shapes"):
         _lib.check(from_logits(300, 256, fake, fake))
+    # the few-row shared expert: 1..8 rows, sizes multiples of 128
+    def shared_rows(tokens, hidden, inter, out):
+        return lib.glm_moe_shared_expert_rows(fake, tokens, hidden, fake, fake, fake, inter, out, fake, 1 << 30, null)
+
+    with pytest.raises(ValueError, match="1 to 8 rows"):
+        _lib.check(shared_rows(9, 6144, 2048, fake))
+    with pytest.raises(ValueError, match="1 to 8 rows"):
+        _lib.check(shared_rows(4, 6144 + 64, 2048, fake))
+    with pytest.raises(ValueError, match="null tensor"):
+        _lib.check(shared_rows(4, 6144, 2048, null))
+    assert lib.glm_moe_shared_expert_rows_workspace_bytes(4, 2048) == 4 * 2048 * 2
     assert lib.glm_moe_uses_decode_kernels(1, 8, 6144, 2048) == 1
     assert lib.glm_moe_uses_decode_kernels(9, 8, 6144, 2048) == 0
     assert lib.glm_moe_uses_decode_kernels(8, 8, 6144, 4096) == 0
