@@ -216,7 +216,8 @@ def full_layer(work, steps, warmup):
     I_shared = I) and the routed experts with the epilogue
     bf16(bf16(routed * 2.5) + shared) fused into their route-sum kernel.  On
     decode shapes the shared expert runs inside the two decode kernels
-    (glm_moe_moe_layer_resident), else as torch GEMMs on hipBLASLt.
+    (glm_moe_moe_layer_resident); for 2-8 rows in the few-row shared-expert
+    kernels (glm_moe_shared_expert_rows); else as torch GEMMs on hipBLASLt.
     Returns (us per layer, algorithmic bytes of the shared expert, how)."""
     import torch
 
@@ -235,8 +236,8 @@ def full_layer(work, steps, warmup):
     out = torch.empty((cfg.tokens, cfg.hidden), dtype=torch.bfloat16, device=device)
     n_rot = len(work.inputs)
 
-    # one row (the decode body): the shared expert inside the decode kernels; more
-    # rows: hipBLASLt, which reads the shared weights once for all of them
+    # one row (the decode body): the shared expert inside the decode kernels; 2-8
+    # rows: the few-row kernels; more: hipBLASLt (each reads the shared weights once)
     resident = work.activations == "bfloat16" and cfg.tokens == 1 and uses_decode_kernels(
         1, cfg.top_k, cfg.hidden, cfg.intermediate)
 
