@@ -87,9 +87,9 @@ __global__ void zero_rows_kernel(uint32_t* out, int64_t rows, int64_t row_words,
 // out = bf16(bf16(routed * routed_scale) + shared), and any non-finite output
 // clears the health byte (:126); every other health writer ran before.
 __global__ void combine_routes_kernel(const uint16_t* y, int64_t tokens, int32_t top_k, int64_t h,
-                                      const int32_t* ids, int32_t experts, int32_t bf16_sum,
-                                      const uint16_t* shared, float routed_scale, uint8_t* valid,
-                                      uint16_t* out) {
+                                      const int32_t* ids, int32_t experts, const float* route_w,
+                                      int32_t bf16_sum, const uint16_t* shared, float routed_scale,
+                                      uint8_t* valid, uint16_t* out) {
   const int64_t groups = h / 8;
   const int64_t total = tokens * groups;
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
@@ -104,10 +104,17 @@ __global__ void combine_routes_kernel(const uint16_t* y, int64_t tokens, int32_t
           if (id < 0 || id >= experts) continue;
         }
         const u32x4 v = *reinterpret_cast<const u32x4*>(y + ((t * top_k + s) * h + c));
+        // bf16 route weight (routed_experts.py:104-105): bf16(bf16(down) * bf16(w))
+        const float w = route_w != nullptr ? round_to_bf16(route_w[t * top_k + s]) : 1.0f;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          acc[2 * j] += bf16_bits_to_f32(v[j] & 0xFFFFu);
-          acc[2 * j + 1] += bf16_bits_to_f32(v[j] >> 16);
+          float lo = bf16_bits_to_f32(v[j] & 0xFFFFu), hi = bf16_bits_to_f32(v[j] >> 16);
+          if (route_w != nullptr) {
+            lo = round_to_bf16(lo * w);
+            hi = round_to_bf16(hi * w);
+          }
+          acc[2 * j] += lo;
+          acc[2 * j + 1] += hi;
           if (bf16_sum) {
             acc[2 * j] = round_to_bf16(acc[2 * j]);
             acc[2 * j + 1] = round_to_bf16(acc[2 * j + 1]);
@@ -333,13 +340,14 @@ hipError_t launch_zero_rows(void* out, int64_t rows, int64_t row_bytes, const ui
 }
 
 hipError_t launch_combine_routes(const uint16_t* y, int64_t tokens, int32_t top_k, int64_t h,
-                                 const int32_t* ids, int32_t experts, int32_t bf16_sum, const uint16_t* shared,
-                                 float routed_scale, uint8_t* valid, uint16_t* out, hipStream_t stream) {
+                                 const int32_t* ids, int32_t experts, const float* route_w, int32_t bf16_sum,
+                                 const uint16_t* shared, float routed_scale, uint8_t* valid, uint16_t* out,
+                                 hipStream_t stream) {
   const int64_t total = tokens * (h / 8);
   if (total == 0) return hipSuccess;
   if (shared != nullptr && valid == nullptr) return hipErrorInvalidValue;
   return launch_kernel(combine_routes_kernel, grid_for(total, 256), dim3(256), 0, stream, y, tokens,
-                     top_k, h, ids, experts, bf16_sum, shared, routed_scale, valid, out);
+                     top_k, h, ids, experts, route_w, bf16_sum, shared, routed_scale, valid, out);
 }
 
 hipError_t launch_count_nonfinite_fp8(const uint8_t* bits, int64_t n, unsigned long long* count,

@@ -367,14 +367,14 @@ int routed_experts_impl(const uint16_t* hidden, int64_t tokens, int64_t hidden_s
   d.ldo = hidden_size;
   d.table_stride = 0;
   d.out_row_ids = sorted;
-  d.route_w = route_weights;
+  d.route_w = nullptr;  // the combine applies the route weights (same rounding, no dependent loads here)
   timer.arm(kStageDown);
-  GLM_HIP(launch_grouped_gemm(d, shape, 1, kEpiWeighted, stream), "down launch");
+  GLM_HIP(launch_grouped_gemm(d, shape, 1, kEpiStoreBf16, stream), "down launch");
   timer.done(kStageDown);
 
   timer.arm(kStageCombine);
   GLM_HIP(launch_combine_routes(y, tokens, top_k, hidden_size,
-                                (flags & GLM_MOE_DROP_UNOWNED) ? route_indices : nullptr, num_experts,
+                                (flags & GLM_MOE_DROP_UNOWNED) ? route_indices : nullptr, num_experts, route_weights,
                                 (flags & GLM_MOE_ROUTE_SUM_BF16) ? 1 : 0, shared, routed_scale, valid, out,
                                 stream),
           "combine launch");

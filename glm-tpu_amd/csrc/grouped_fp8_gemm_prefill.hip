@@ -282,7 +282,8 @@ __global__ __launch_bounds__(64 * WAVES, 1) void prefill_gemm_kernel(const Group
     };
 
     // output rows of this lane's route columns, loaded ahead of the streams so
-    // the epilogue waits at most for the weighted epilogue's route weights
+    // the epilogue waits for no load (the layer's route weights are applied by
+    // the combine, not here)
     int orow[NCG];
     load_out_rows(a, r0, live, lrow, orow);
 
@@ -675,12 +676,12 @@ hipError_t launch_grouped_gemm_prefill(const GroupedGemmArgs& a, int tables, int
     if (a.xscale == nullptr) return hipErrorInvalidValue;
     if (tables == 2 && epilogue == kEpiSwiglu)
       return launch_prefill_fp8<2, 1, 8, kEpiSwiglu>(a, stream);
-    if (tables == 1 && epilogue == kEpiWeighted)
-      return launch_prefill_fp8<1, 2, 8, kEpiWeighted>(a, stream);
+    if (tables == 1 && epilogue == kEpiStoreBf16)
+      return launch_prefill_fp8<1, 2, 8, kEpiStoreBf16>(a, stream);
     return hipErrorInvalidValue;
   }
   if (tables == 2 && epilogue == kEpiSwiglu) return launch_prefill<2, 1, 8, kEpiSwiglu>(a, stream);
-  if (tables == 1 && epilogue == kEpiWeighted) return launch_prefill<1, 2, 8, kEpiWeighted>(a, stream);
+  if (tables == 1 && epilogue == kEpiStoreBf16) return launch_prefill<1, 2, 8, kEpiStoreBf16>(a, stream);
   return hipErrorInvalidValue;
 }
 

@@ -242,12 +242,14 @@ hipError_t launch_pack_panel_rows(const void* src, int64_t src_rows, int64_t row
 hipError_t launch_zero_rows(void* out, int64_t rows, int64_t row_bytes, const uint8_t* keep,
                             const uint8_t* valid, hipStream_t stream);
 // out[t] = bf16(sum over slots of y[t * top_k + s]); with ids != nullptr a slot
-// whose raw id is outside [0, experts) contributes nothing (decode ownership).
+// whose raw id is outside [0, experts) contributes nothing (decode ownership);
+// with route_w != nullptr slot s contributes bf16(y * bf16(route_w[t * top_k + s])).
 // shared: null, or the layer epilogue's bf16 shared-expert rows (out =
 // bf16(bf16(routed * routed_scale) + shared), and a non-finite output clears valid).
 hipError_t launch_combine_routes(const uint16_t* y, int64_t tokens, int32_t top_k, int64_t h,
-                                 const int32_t* ids, int32_t experts, int32_t bf16_sum, const uint16_t* shared,
-                                 float routed_scale, uint8_t* valid, uint16_t* out, hipStream_t stream);
+                                 const int32_t* ids, int32_t experts, const float* route_w, int32_t bf16_sum,
+                                 const uint16_t* shared, float routed_scale, uint8_t* valid, uint16_t* out,
+                                 hipStream_t stream);
 // GLM noaux_tc routing of [tokens, experts] FP32 logits (experts <= 1024, top_k <= 16).
 // Adds the count of e4m3fn NaN bytes (0x7F / 0xFF) among n bytes to *count.
 hipError_t launch_count_nonfinite_fp8(const uint8_t* bits, int64_t n, unsigned long long* count,
