@@ -204,7 +204,7 @@ def test_algorithmic_bytes_of_the_decode_config():
     ids, _ = S.routes(cfg, 0)
     b = S.algorithmic_bytes(cfg, ids)
     assert b["distinct_experts"] == 8
-    # 8 experts x 3 x 6144 x 2048 e4m3 bytes + scales + activations (302.1 MB)
+    # 8 experts x 3 x 6144 x 2048 e4m3 bytes + scales + activations: 302.1 MB
     assert abs(b["total"] - 302.1e6) < 0.1e6
     assert S.algorithmic_flops(cfg)["total"] == 2 * 8 * 3 * 6144 * 2048
 
