@@ -47,7 +47,6 @@ constexpr int kNonTemporal = 2;             // buffer load cache policy: streame
 constexpr int kBufferFormat = 0x00020000;   // raw buffer descriptor word 3: 32-bit data format
 
 constexpr int kBM = 128;           // routes per tile
-constexpr int kCG = kBM / 16;      // 16-route column groups
 constexpr int kXcds = 8;           // MI355X: 8 XCDs, workgroups dealt round-robin
 constexpr int kRowBytes = kScaleBlock * 2;   // one staged activation row of a K block (bf16)
 

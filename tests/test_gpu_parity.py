@@ -534,6 +534,34 @@ def test_decode_production_shape_matches_oracle(device, production_tables, name)
     np.testing.assert_array_equal(bf16_bits_of(again), bf16_bits_of(out))  # deterministic
 
 
+@pytest.mark.parametrize("top_k,unowned", [(6, False), (5, False), (8, True), (3, True)])
+def test_decode_production_shape_ragged_route_pairs(device, production_tables, top_k, unowned):
+    """One token at I = 2048 with fewer than 8 active routes (top-k below 8, or an
+    unowned route dropped): the down kernel's four waves take two routes each
+    where they exist and one or none elsewhere."""
+    from glm_moe import synthetic as S
+    from glm_moe.layers.moe.routed_experts import routed_experts
+
+    cfg = S.CONFIGS["decode_t1"]
+    x = S.hidden_states(cfg, 5)
+    ids, w = S.routes(cfg, 5)
+    ids, w = np.ascontiguousarray(ids[:, :top_k]), np.ascontiguousarray(w[:, :top_k])
+    t = production_tables
+    host, local_ids = _subproblem(t, ids)
+    if unowned:
+        ids = ids.copy()
+        ids[0, 1] = cfg.experts + 7  # outside [0, E): dropped from the sum
+        local_ids = local_ids.copy()
+        local_ids[0, 1] = -1
+    kw = dict(drop_unowned=True, check_weights=False, route_sum="bfloat16") if unowned else {}
+    out, ok = routed_experts(bf16_dev(x, device), dev(ids, device), dev(w, device), *(t[k] for k in TABLE_KEYS),
+                             **kw)
+    ref, _ = O.routed_experts(x, local_ids, w, **host, **kw)
+    if not unowned:
+        assert bool(ok)
+    print(top_k, unowned, assert_moe_close(host_f32(out), ref))
+
+
 @pytest.mark.parametrize("name", ["prefill_t2048", "prefill_t8192_zipf"])
 def test_prefill_production_shape_sampled_tokens(device, production_tables, name):
     """Full-size prefill; each output row depends only on its token's routes, so
