@@ -92,3 +92,42 @@ def test_graph_replays_of_the_layer_from_router_logits_match_eager():
         torch.cuda.synchronize()
         for got, want in zip(captured, eager):
             assert torch.equal(got, want), f"replay {replay} differs from the eager result"
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("tokens", [2, 4, 8])
+def test_graph_replays_of_the_few_row_shared_expert_match_eager(tokens):
+    """The few-row shared expert feeding the layer's fused epilogue, as the batched
+    decode layer runs it, captured and replayed with other rows computed eagerly
+    between replays."""
+    from glm_moe.layers.moe.routed_experts import routed_experts, shared_expert_rows
+
+    hidden, inter = 768, 384
+    x, ids, w, tables = _case(tokens, 16, hidden, inter, 8, seed=tokens + 20)
+    x2, ids2, w2, _ = _case(tokens, 16, hidden, inter, 8, seed=tokens + 21)
+    g = torch.Generator(device="cuda").manual_seed(3)
+    sg, su, sd = ((torch.randn(s, generator=g, device="cuda") * 0.05).to(torch.bfloat16)
+                  for s in ((inter, hidden), (inter, hidden), (hidden, inter)))
+    out = torch.empty((tokens, hidden), dtype=torch.bfloat16, device="cuda")
+
+    def layer(xx, ii, ww):
+        shared = shared_expert_rows(xx, sg, su, sd)
+        return routed_experts(xx, ii, ww, *tables, out=out, shared=shared, routed_scale=2.5)
+
+    eager, ok = layer(x, ids, w)
+    eager = eager.clone()
+    other, _ = layer(x2, ids2, w2)
+    other = other.clone()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        _, valid = layer(x, ids, w)
+    for replay in range(3):
+        out.zero_()
+        layer(x2, ids2, w2)  # eager work into the same output buffer
+        torch.cuda.synchronize()
+        assert torch.equal(out, other)
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), f"replay {replay} differs from the eager result"
+        assert bool(valid) == bool(ok)
