@@ -144,6 +144,7 @@ constexpr int prefill_pending(int sw, int sx, int xloads, int wloads) {
 
 template <int TABLES, int RG, int WAVES, int EPI>
 __global__ __launch_bounds__(64 * WAVES, 1) void prefill_gemm_kernel(const GroupedGemmArgs a) {
+  static_assert(EPI != kEpiWeighted, "the layer's route weights are applied by the combine, not here");
   constexpr int BN = WAVES * RG * 16;  // weight rows per table per work item
   constexpr int GROUPS = TABLES * RG;  // 16-row weight groups of one wave
   constexpr int WLOADS = GROUPS * 2;   // 1 KB weight loads per wave per K block
@@ -368,14 +369,11 @@ __global__ __launch_bounds__(64 * WAVES, 1) void prefill_gemm_kernel(const Group
     int64_t orow_ok[NCG];
 #pragma unroll
     for (int cg = 0; cg < NCG; ++cg) orow_ok[cg] = out_row(a, cg * 16 + lrow, live, orow[cg]);
-    float wgt[NCG];  // every route weight load in flight at once
-#pragma unroll
-    for (int cg = 0; cg < NCG; ++cg) wgt[cg] = fragment_weight<EPI>(a, orow_ok[cg]);
 #pragma unroll
     for (int cg = 0; cg < NCG; ++cg)
 #pragma unroll
       for (int rg = 0; rg < RG; ++rg)
-        store_fragment_at<TABLES, EPI>(a, orow_ok[cg], wgt[cg], n0 + rg * 16 + lgrp * 4, acc[0][rg][cg],
+        store_fragment_at<TABLES, EPI>(a, orow_ok[cg], 1.0f, n0 + rg * 16 + lgrp * 4, acc[0][rg][cg],
                                        acc[TABLES - 1][rg][cg]);
   };
   switch (ncg) {
@@ -421,6 +419,7 @@ struct Fp8Rings {
 
 template <int TABLES, int RG, int WAVES, int EPI>
 __global__ __launch_bounds__(64 * WAVES, 1) void prefill_gemm_fp8_kernel(const GroupedGemmArgs a) {
+  static_assert(EPI != kEpiWeighted, "the layer's route weights are applied by the combine, not here");
   constexpr int BN = WAVES * RG * 16;
   constexpr int GROUPS = TABLES * RG;
   constexpr int WLOADS = GROUPS * 2;
@@ -610,14 +609,11 @@ __global__ __launch_bounds__(64 * WAVES, 1) void prefill_gemm_fp8_kernel(const G
     int64_t orow_ok[NCG];
 #pragma unroll
     for (int cg = 0; cg < NCG; ++cg) orow_ok[cg] = out_row(a, cg * 16 + lrow, live, orow[cg]);
-    float wgt[NCG];  // every route weight load in flight at once
-#pragma unroll
-    for (int cg = 0; cg < NCG; ++cg) wgt[cg] = fragment_weight<EPI>(a, orow_ok[cg]);
 #pragma unroll
     for (int cg = 0; cg < NCG; ++cg)
 #pragma unroll
       for (int rg = 0; rg < RG; ++rg)
-        store_fragment_at<TABLES, EPI>(a, orow_ok[cg], wgt[cg], n0 + rg * 16 + lgrp * 4, acc[0][rg][cg],
+        store_fragment_at<TABLES, EPI>(a, orow_ok[cg], 1.0f, n0 + rg * 16 + lgrp * 4, acc[0][rg][cg],
                                        acc[TABLES - 1][rg][cg]);
   };
   switch (ncg) {
