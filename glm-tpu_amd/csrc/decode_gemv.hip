@@ -48,6 +48,8 @@ constexpr int kGateUpDepth = 2;    // two tables: 2 x 32 VGPRs in flight
 constexpr int kDownRows = 8;       // down: weight rows per workgroup (H / 8 = 768 workgroups: 3 per CU)
 constexpr int kDownQuads = kDownRows / 4;
 constexpr int kDownDepth = 6;      // one table, 8 rows: 6 x 8 VGPRs in flight
+constexpr int kSharedGateUpRows = 8;   // resident shared expert: bf16 gate/up rows per workgroup
+constexpr int kSharedGateUpDepth = 4;  // 2 tables x 8 bf16 rows: 4 steps (4 x 16 VGPRs) in flight
 
 constexpr int kNonTemporal = 2;            // buffer load cache policy: streamed once (nt)
 constexpr int kBufferFormat = 0x00020000;  // raw buffer descriptor word 3: 32-bit data format
@@ -402,8 +404,11 @@ void decode_gate_up_kernel(const DecodeArgs a, int wave_steps) {
   const int I = a.intermediate, H = a.hidden;
   const int row0 = blockIdx.y * kGemvRows;
   if ((int)blockIdx.x >= a.routes) {
-    // the resident shared expert of token blockIdx.x - routes: bf16 gate/up + SwiGLU
-    const int t = blockIdx.x - a.routes;
+    // the resident shared expert of token (blockIdx.x - routes) / 2: bf16 gate/up +
+    // SwiGLU of 8 of the row block's 16 rows, so that a shared workgroup streams
+    // as many bytes as a routed one (8 bf16 rows = 16 e4m3 rows)
+    const int t = (blockIdx.x - a.routes) >> 1;
+    const int srow0 = row0 + kSharedGateUpRows * ((blockIdx.x - a.routes) & 1);
     const int ws = bf16_wave_steps(H, WK);
     Bf16Stream<2> g;
     g.k = H;
@@ -411,29 +416,32 @@ void decode_gate_up_kernel(const DecodeArgs a, int wave_steps) {
     g.lane_off = (uint32_t)((lane >> 4) * 2 * H + (lane & 15) * 16);
     g.step_begin = min(wk * ws, H / kBf16StepK);
     g.step_end = min(g.step_begin + ws, H / kBf16StepK);
-    g.w[0] = rows_buffer(reinterpret_cast<const uint8_t*>(a.shared_gate + (int64_t)row0 * H), (int64_t)kGemvRows * 2 * H);
-    g.w[1] = rows_buffer(reinterpret_cast<const uint8_t*>(a.shared_up + (int64_t)row0 * H), (int64_t)kGemvRows * 2 * H);
+    g.w[0] = rows_buffer(reinterpret_cast<const uint8_t*>(a.shared_gate + (int64_t)srow0 * H),
+                         (int64_t)kSharedGateUpRows * 2 * H);
+    g.w[1] = rows_buffer(reinterpret_cast<const uint8_t*>(a.shared_up + (int64_t)srow0 * H),
+                         (int64_t)kSharedGateUpRows * 2 * H);
     g.x = a.hidden_in + (int64_t)t * H;
     g.xs = reinterpret_cast<uint16_t*>(smem + sizeof(float) * WK * 2 * kGemvRows) + wk * xs_elems(wave_steps);
-    float acc[2][4] = {};
-    bf16_run<kGateUpDepth>(g, lane, acc);
+    constexpr int QN = kSharedGateUpRows / 4;
+    float acc[2][QN] = {};
+    bf16_run<kSharedGateUpDepth>(g, lane, acc);
 #pragma unroll
     for (int tb = 0; tb < 2; ++tb)
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
+      for (int q = 0; q < QN; ++q) {
         const float v = sum16(acc[tb][q]);
         if ((lane & 15) == 0) red[wk][tb][4 * q + (lane >> 4)] = v;
       }
     __syncthreads();
     const int tid = threadIdx.x;
-    if (tid < kGemvRows) {
+    if (tid < kSharedGateUpRows) {
       float gsum = 0.f, usum = 0.f;
       for (int w = 0; w < WK; ++w) {
         gsum += red[w][0][tid];
         usum += red[w][1][tid];
       }
       const float v = swiglu_bf16(round_to_bf16(gsum), round_to_bf16(usum));
-      a.act_shared[(int64_t)t * I + row0 + tid] = f32_to_bf16_bits(v);
+      a.act_shared[(int64_t)t * I + srow0 + tid] = f32_to_bf16_bits(v);
     }
     return;
   }
@@ -809,7 +817,7 @@ hipError_t launch_decode_routed(const DecodeArgs& a, hipStream_t stream, const L
                    a.intermediate > xs_elems((a.intermediate + kStepK - 1) / kStepK)))
     return hipErrorInvalidValue;
   const int tokens = a.routes / a.top_k;
-  const dim3 g1(a.routes + (resident ? tokens : 0), a.intermediate / kGemvRows);
+  const dim3 g1(a.routes + (resident ? 2 * tokens : 0), a.intermediate / kGemvRows);
   if (stage_events) next_launch_events() = stage_events[0];
   hipError_t err = launch_kernel(decode_gate_up_kernel<kGateUpWaves>, g1, dim3(64 * kGateUpWaves), gu_lds, stream,
                                  a, gu_steps);
