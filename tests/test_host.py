@@ -59,6 +59,33 @@ def test_library_exports_every_declared_symbol():
     assert _lib.lib().glm_moe_abi_version() == 1
 
 
+def test_ctypes_signatures_match_the_header_parameter_lists():
+    """Every binding passes as many arguments as its C declaration takes, and
+    every declaration in the header has a definition of the same parameter
+    types in the C ABI source."""
+    import re
+    from pathlib import Path
+
+    from glm_moe import _lib
+
+    root = Path(__file__).resolve().parents[1]
+
+    def declarations(text):
+        out = {}
+        for m in re.finditer(r"\b(?:int|size_t|const char\*)\s+(glm_moe_\w+)\s*\(([^)]*)\)", text):
+            params = [p.strip() for p in m.group(2).split(",") if p.strip() and p.strip() != "void"]
+            out[m.group(1)] = [re.sub(r"\s*\w+$", "", p).replace(" ", "") for p in params]
+        return out
+
+    header = declarations((root / "include" / "glm_moe.h").read_text())
+    source = declarations((root / "glm-tpu_amd" / "csrc" / "capi.hip").read_text())
+    assert header and set(header) <= set(source)
+    for name, types in header.items():
+        assert source[name] == types, name
+        _, argtypes = _lib.SIGNATURES[name]
+        assert len(argtypes) == len(types), name
+
+
 def test_workspace_sizes_are_host_computable():
     from glm_moe import _lib
 
