@@ -439,6 +439,8 @@ def _small_case(tokens, experts, hidden, inter, top_k, zipf, seed):
 
 @pytest.mark.parametrize("tokens,experts,hidden,inter,top_k,zipf", [
     (3, 16, 512, 256, 4, 0.0),      # skinny (decode-like), several experts
+    (8, 64, 512, 256, 8, 0.0),      # 64 routes: the decode kernels' maximum
+    (9, 64, 512, 256, 8, 0.0),      # 72 routes: the first size on the grouped path
     (64, 32, 768, 384, 8, 0.0),     # skinny with multi-route experts
     (512, 16, 512, 256, 8, 1.2),    # wide path, skewed: multi-tile experts
     (300, 64, 256, 512, 6, 0.0),    # wide path, ragged tiles

@@ -254,3 +254,13 @@ def test_router_refuses_bad_geometry():
         route_glm_noaux_tc_logits(torch.zeros(2, 8), torch.zeros(8), top_k=9)
     with pytest.raises(ValueError, match="GPU tensors only"):
         route_glm_noaux_tc_logits(torch.zeros(2, 8), torch.zeros(8), top_k=2)
+
+
+def test_decode_kernels_take_at_most_64_routes():
+    from glm_moe.layers.moe.routed_experts import uses_decode_kernels
+
+    assert uses_decode_kernels(1, 8, 6144, 2048)
+    assert uses_decode_kernels(8, 8, 512, 256)       # 64 routes
+    assert not uses_decode_kernels(9, 8, 512, 256)   # 72 routes: route plan + grouped GEMMs
+    assert uses_decode_kernels(64, 1, 512, 256)
+    assert not uses_decode_kernels(65, 1, 512, 256)
