@@ -432,27 +432,22 @@ def dominant_roofline(cfg, head):
     return line
 
 
-def fp8_error(work, device, rows=2):
-    """Error of the native FP8 mode against the reference numerics (the bf16
-    oracle) on `rows` sampled tokens of the workload's first routing."""
-    import torch
-
+def fp8_error(work, device):
+    """Error of the native FP8 mode against the reference numerics: the same
+    layer on the library's bf16 path (decoded weights, bf16 activations; the
+    GPU parity tests hold it to the oracle within max-abs 2e-2 / mean-rel 5e-3),
+    over every token of the workload's first routing."""
     from glm_moe.layers.moe.routed_experts import routed_experts
-    from oracle import moe_oracle as O
 
-    x, ids, w = work.host[0]
     xd, idd, wd = work.inputs[0]
-    out, _ = routed_experts(xd, idd, wd, *[work.tables[k] for k in TABLE_KEYS], activations="float8_e4m3fn")
-    got = out.float().cpu().numpy()
-    pick = np.random.default_rng(0).choice(x.shape[0], rows, replace=False)
-    used = np.unique(ids[pick].reshape(-1))
-    index = torch.as_tensor(used, dtype=torch.long, device=device)
-    host = {k: work.tables[k].index_select(0, index).cpu().numpy() for k in TABLE_KEYS}
-    remap = np.searchsorted(used, ids[pick]).astype(np.int32)
-    ref, _ = O.routed_experts(x[pick], remap, w[pick], **host)
-    err = np.abs(got[pick].astype(np.float64) - ref)
-    return {"max_abs": float(err.max()), "mean_rel": float(err.mean() / np.abs(ref).mean()),
-            "sample": f"{rows} tokens vs the bf16 oracle (reference numerics)"}
+    tables = [work.tables[k] for k in TABLE_KEYS]
+    got, _ = routed_experts(xd, idd, wd, *tables, activations="float8_e4m3fn")
+    ref, _ = routed_experts(xd, idd, wd, *tables)
+    got = got.double()
+    ref = ref.double()
+    err = (got - ref).abs()
+    return {"max_abs": float(err.max()), "mean_rel": float(err.mean() / ref.abs().mean()),
+            "sample": f"all {xd.shape[0]} tokens vs the bf16 path (reference numerics)"}
 
 
 def cpu_baseline(work, device):
