@@ -67,7 +67,9 @@ def build(verbose: bool = True) -> Path:
     with cf.ThreadPoolExecutor(max_workers=workers) as pool:
         objects = list(pool.map(_compile, sources))
     tmp = LIB.with_suffix(".so.tmp")
-    cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objects), "-o", str(tmp)]
+    # roctx: each launch's shape-suffixed profiler name (rocprofv3 --kernel-rename)
+    cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objects), "-lrocprofiler-sdk-roctx",
+           "-o", str(tmp)]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
         raise RuntimeError("link failed:\n" + proc.stdout + proc.stderr)

@@ -425,6 +425,7 @@ hipError_t launch_synth_fp8(uint64_t seed, int32_t experts, int64_t n, int64_t k
                             uint8_t* bits, float* scales, hipStream_t stream) {
   const int64_t blocks = (int64_t)experts * (n / 128) * (k / 128);
   if (blocks == 0) return hipSuccess;
+  label_next_launch("synthesize_fp8_weights_e%d_n%lld_k%lld", experts, (long long)n, (long long)k);
   return launch_kernel(synth_fp8_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, seed, n, k, sigma,
                      bits, scales);
 }
@@ -433,6 +434,7 @@ hipError_t launch_decode_fp8_table(const uint8_t* bits, const float* scale, int6
                                    int32_t block_n, int32_t block_k, uint16_t* out,
                                    hipStream_t stream) {
   if (n * k == 0) return hipSuccess;
+  label_next_launch("decode_fp8_table_n%lld_k%lld", (long long)n, (long long)k);
   return launch_kernel(decode_fp8_table_kernel, grid_for(n * k, 256), dim3(256), 0, stream, bits, scale,
                      n, k, block_n, block_k, out);
 }
@@ -441,6 +443,7 @@ hipError_t launch_swiglu_bf16(const uint16_t* g, const uint16_t* u, int64_t n, u
   if (n == 0) return hipSuccess;
   const bool aligned = ((reinterpret_cast<uintptr_t>(g) | reinterpret_cast<uintptr_t>(u) |
                          reinterpret_cast<uintptr_t>(out)) & 15) == 0;
+  label_next_launch("swiglu_bf16_n%lld", (long long)n);
   if (aligned && n % 8 == 0)
     return launch_kernel(swiglu_bf16_x8_kernel, grid_for(n / 8, 256), dim3(256), 0, stream,
                          reinterpret_cast<const u32x4*>(g), reinterpret_cast<const u32x4*>(u), n / 8,
@@ -453,6 +456,7 @@ hipError_t launch_gather_rows(const void* src, int64_t src_rows, int64_t row_byt
                               void* dst, hipStream_t stream) {
   const int64_t words = row_bytes / 4;
   if (n * words == 0) return hipSuccess;
+  label_next_launch("gather_prefill_route_rows_r%lld_b%lld", (long long)n, (long long)row_bytes);
   return launch_kernel(gather_rows_kernel, grid_for(n * words, 256), dim3(256), 0, stream,
                      static_cast<const uint32_t*>(src), src_rows, words, index, div, mask, n,
                      static_cast<uint32_t*>(dst));
@@ -465,6 +469,7 @@ hipError_t launch_pack_panel_rows(const void* src, int64_t src_rows, int64_t row
   const int64_t words = row_bytes / 4;
   const int64_t total = (int64_t)capacity * panel_rows * words;
   if (total == 0) return hipSuccess;
+  label_next_launch("pack_expert_panel_rows_p%d_b%lld", capacity, (long long)row_bytes);
   return launch_kernel(pack_panel_rows_kernel, grid_for(total, 256), dim3(256), 0, stream,
                      static_cast<const uint32_t*>(src), src_rows, words, row_starts, live_counts,
                      capacity, panel_rows, static_cast<uint32_t*>(dst));
@@ -474,6 +479,7 @@ hipError_t launch_zero_rows(void* out, int64_t rows, int64_t row_bytes, const ui
                             const uint8_t* valid, hipStream_t stream) {
   const int64_t words = row_bytes / 4;
   if (rows * words == 0) return hipSuccess;
+  label_next_launch("unpack_expert_panel_rows_r%lld_b%lld", (long long)rows, (long long)row_bytes);
   return launch_kernel(zero_rows_kernel, grid_for(rows * words, 256), dim3(256), 0, stream,
                      static_cast<uint32_t*>(out), rows, words, keep, valid);
 }
@@ -486,6 +492,8 @@ hipError_t launch_combine_routes(const uint16_t* y, int64_t tokens, int32_t top_
   if (total == 0) return hipSuccess;
   if (h % 8 != 0 || (shared != nullptr && valid == nullptr) || (out_f32 != nullptr && shared != nullptr))
     return hipErrorInvalidValue;
+  label_next_launch("restore_prefill_route_rows_t%lld_k%d_h%lld%s", (long long)tokens, top_k, (long long)h,
+                    shared != nullptr ? "_epilogue" : "");
   return launch_kernel(combine_routes_kernel, grid_for(total, 256), dim3(256), 0, stream, y, tokens,
                      top_k, h, ids, own, route_w, shared, routed_scale, valid, out, out_f32, round_partial);
 }
@@ -495,6 +503,7 @@ hipError_t launch_layer_epilogue(const float* routed, int64_t tokens, int64_t h,
   const int64_t total = tokens * (h / 8);
   if (total == 0) return hipSuccess;
   if (h % 8 != 0 || valid == nullptr) return hipErrorInvalidValue;
+  label_next_launch("moe_layer_epilogue_t%lld_h%lld", (long long)tokens, (long long)h);
   return launch_kernel(layer_epilogue_kernel, grid_for(total, 256), dim3(256), 0, stream, routed, tokens, h,
                        shared, routed_scale, valid, out);
 }
@@ -504,6 +513,7 @@ hipError_t launch_count_nonfinite_fp8(const uint8_t* bits, int64_t n, unsigned l
   if (n <= 0) return hipSuccess;
   const int64_t words = (n >> 2) > 0 ? (n >> 2) : 1;
   const int64_t blocks = words / 256 + 1 < 4096 ? words / 256 + 1 : 4096;
+  label_next_launch("count_nonfinite_fp8_n%lld", (long long)n);
   return launch_kernel(count_nonfinite_fp8_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, bits, n, count);
 }
 
@@ -513,6 +523,7 @@ hipError_t launch_route_noaux_tc(const float* logits, int64_t tokens, int32_t ex
   if (experts <= 0 || experts > kMaxExperts || top_k <= 0 || top_k > kWave || top_k > experts)
     return hipErrorInvalidValue;
   const int64_t blocks = (tokens + 3) / 4;
+  label_next_launch("route_glm_noaux_tc_t%lld_e%d_k%d", (long long)tokens, experts, top_k);
   if (experts <= 256)
     return launch_kernel(route_noaux_tc_kernel<4>, dim3((unsigned)blocks), dim3(256), 0, stream, logits, tokens,
                          experts, bias, top_k, ids, weights);
@@ -525,6 +536,7 @@ hipError_t launch_quantize_rows_fp8(const uint16_t* x, int64_t rows, int64_t k, 
   if (rows <= 0 || k <= 0) return hipSuccess;
   if (k % 128 != 0 || per_row < 1 || per_row > 64 || (positions == nullptr && per_row != 1)) return hipErrorInvalidValue;
   const int64_t blocks = rows * (k / 128);
+  label_next_launch("quantize_rows_fp8_r%lld_k%lld", (long long)rows, (long long)k);
   if (((reinterpret_cast<uintptr_t>(x) & 15) | (reinterpret_cast<uintptr_t>(q) & 7)) == 0) {
     const int64_t wgs = (blocks + 15) / 16;  // 16 blocks a workgroup
     return launch_kernel(quantize_rows_fp8_x8_kernel, dim3((unsigned)(wgs < 65536 ? wgs : 65536)), dim3(256), 0,

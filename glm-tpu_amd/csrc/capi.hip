@@ -23,6 +23,18 @@ LaunchEvents& next_launch_events() {
   return armed;
 }
 
+char* next_launch_label() {
+  thread_local char label[kLabelBytes] = {};
+  return label;
+}
+
+void label_next_launch(const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(next_launch_label(), kLabelBytes, fmt, ap);
+  va_end(ap);
+}
+
 }  // namespace glm_moe
 
 namespace {
@@ -36,6 +48,7 @@ int fail(int status, const char* fmt, ...) {
   vsnprintf(buf, sizeof(buf), fmt, ap);
   va_end(ap);
   g_last_error = buf;
+  next_launch_label()[0] = '\0';  // a refused call's label must not name a later launch
   return status;
 }
 
@@ -290,7 +303,14 @@ int routed_experts_impl(const uint16_t* hidden, int64_t tokens, int64_t hidden_s
     d.valid = valid;
     d.shared = shared;
     d.routed_scale = routed_scale;
-    if (router != nullptr) {
+    if (router != nullptr && num_experts > kDecodeRouterExperts) {
+      // the decode gate/up kernel routes at most kDecodeRouterExperts experts:
+      // the router kernel runs ahead of it (after every check above, so a
+      // refused call has launched nothing and left the route outputs alone)
+      GLM_HIP(launch_route_noaux_tc(router->logits, tokens, num_experts, router->bias, top_k,
+                                    const_cast<int32_t*>(route_indices), const_cast<float*>(route_weights), stream),
+              "router launch");
+    } else if (router != nullptr) {
       d.router_logits = router->logits;
       d.router_bias = router->bias;
       d.ids_out = const_cast<int32_t*>(route_indices);
@@ -482,10 +502,22 @@ constexpr int kScratchDevices = 64;
 std::mutex g_scratch_mutex;
 void* g_scratch_ptr[kScratchDevices] = {};
 
-// This device's copy of `scratch` (looked up on the first call on the device).
-int static_scratch(void** out) {
+// The copy of `scratch` on the device the call's kernels run on (looked up on
+// the first call on the device).  Kernels run on the stream's device, but the
+// symbol's address is taken for the current device, so a stream of another
+// device than the current one is refused (the null stream runs on the current
+// device).
+int static_scratch(hipStream_t stream, void** out) {
   int dev = 0;
   GLM_HIP(hipGetDevice(&dev), "hipGetDevice");
+  if (stream != nullptr) {
+    hipDevice_t stream_dev = 0;
+    GLM_HIP(hipStreamGetDevice(stream, &stream_dev), "hipStreamGetDevice");
+    GLM_REQUIRE(stream_dev == dev,
+                "the stream runs on device %d but device %d is current: make the stream's device current "
+                "(the static scratch is looked up per device)",
+                (int)stream_dev, dev);
+  }
   GLM_REQUIRE(dev >= 0 && dev < kScratchDevices, "device %d beyond the %d the static scratch tracks", dev,
               kScratchDevices);
   std::lock_guard<std::mutex> lock(g_scratch_mutex);
@@ -721,6 +753,7 @@ int glm_moe_routed_projection(const uint16_t* lhs, int32_t slots, int64_t k, int
                             tile_count, s),
           "slot plan launch");
   GroupedGemmArgs g{};
+  g.name = "fp8_routed_projection";
   g.experts = experts;
   g.rows = slots;
   g.x_rows = slots;
@@ -812,19 +845,10 @@ int glm_moe_moe_layer_from_router_logits(const uint16_t* hidden, int64_t tokens,
               (int)num_experts);
   GLM_REQUIRE(shared == nullptr || std::isfinite(routed_scale), "routed scale must be finite");
   const RouterIn router{router_logits, correction_bias};
-  const RouterIn* fused = &router;
-  if (tokens > 0 && top_k > 0 && uses_decode_path(tokens * top_k, hidden_size, intermediate) &&
-      num_experts > kDecodeRouterExperts) {
-    // the decode gate/up kernel routes at most kDecodeRouterExperts experts
-    GLM_HIP(launch_route_noaux_tc(router_logits, tokens, num_experts, correction_bias, top_k, route_indices,
-                                  route_weights, as_stream(stream)),
-            "router launch");
-    fused = nullptr;
-  }
   return routed_experts_impl(hidden, tokens, hidden_size, route_indices, route_weights, top_k, num_experts,
                              intermediate, gate_bits, gate_scale, up_bits, up_scale, down_bits, down_scale, flags,
                              shared, nullptr, shared ? bf16_round_host(routed_scale) : 0.0f, out, valid, workspace,
-                             workspace_bytes, StageTimer{nullptr, nullptr}, stream, fused);
+                             workspace_bytes, StageTimer{nullptr, nullptr}, stream, &router);
 }
 
 int glm_moe_routed_experts_share(const uint16_t* hidden, int64_t tokens, int64_t hidden_size,
@@ -908,7 +932,7 @@ int glm_moe_moe_layer_resident_noalloc(const uint16_t* hidden, int64_t tokens, i
               "the allocation-free layer has %zu bytes of static scratch per device; this call needs %zu",
               kStaticScratchBytes, need);
   void* ws = nullptr;
-  const int st = static_scratch(&ws);
+  const int st = static_scratch(as_stream(stream), &ws);
   if (st != GLM_MOE_OK) return st;
   const uint16_t* resident[3] = {shared_gate, shared_up, shared_down};
   return routed_experts_impl(hidden, tokens, hidden_size, route_indices, route_weights, top_k,

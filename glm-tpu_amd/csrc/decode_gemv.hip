@@ -757,6 +757,7 @@ hipError_t launch_shared_rows(const uint16_t* x, int k, const uint16_t* w0, cons
   if (err != hipSuccess) return err;
   const size_t lds = sizeof(float) * kSharedWaves * TABLES * kSharedWgRows * NT +
                      sizeof(uint16_t) * kSharedWaves * NT * shared_wave_steps(k) * kBf16StepK;
+  label_next_launch("shared_expert_rows_s%d_t%d_k%d_n%d", NT, TABLES, k, n);
   return launch_kernel(shared_rows_kernel<TABLES, NT>, dim3(n / kSharedWgRows), dim3(64 * kSharedWaves), lds, stream,
                        x, k, w0, w1, n, out);
 }
@@ -832,6 +833,10 @@ hipError_t launch_decode_routed(const DecodeArgs& a, hipStream_t stream, const L
   const int tokens = a.routes / a.top_k;
   const dim3 g1(a.routes + (resident ? 2 * tokens : 0), a.intermediate / kGemvRows);
   if (stage_events) next_launch_events() = stage_events[0];
+  // the reference's decode kernel name: routes (slots), tables, K, N, the
+  // intermediate rows of a workgroup and the K of one load step
+  label_next_launch("fp8_routed_projection_s%d_t2_k%d_n%d_tn%d_tk%d%s%s", a.routes, a.hidden, a.intermediate,
+                    kGemvRows, kStepK, resident ? "_shared" : "", a.router_logits != nullptr ? "_router" : "");
   hipError_t err = launch_kernel(decode_gate_up_kernel<kGateUpWaves>, g1, dim3(64 * kGateUpWaves), gu_lds, stream,
                                  a, gu_steps);
   if (err != hipSuccess) return err;
@@ -845,6 +850,8 @@ hipError_t launch_decode_routed(const DecodeArgs& a, hipStream_t stream, const L
                        sizeof(uint16_t) * d_waves * xs_elems(d_steps) +
                        (resident ? sizeof(float) * kMaxDecodeRoutes * kGemvRows : 0);
   if (stage_events) next_launch_events() = stage_events[1];
+  label_next_launch("fp8_routed_projection_s%d_t1_k%d_n%d_tn%d_tk%d%s", a.routes, a.intermediate, a.hidden, kDownRows,
+                    kStepK, resident ? "_shared" : "");
   if (resident)
     return launch_kernel(decode_down_kernel<kDownWaves, true>, dim3(a.hidden / kDownRows), dim3(64 * kDownWaves),
                          d_lds, stream, a);

@@ -230,6 +230,7 @@ hipError_t launch_shape(const GroupedGemmArgs& a, int epilogue, hipStream_t stre
   constexpr int BN = WN * RG * 16;
   const dim3 grid(a.max_tiles, a.n / BN);
   const dim3 block(64 * WN * WK);
+  label_grouped_gemm(a, TABLES, XROWS, BN, "");
   switch (epilogue) {
     case kEpiStoreF32:
       return launch_kernel(grouped_fp8_gemm_kernel<TABLES, RG, XROWS, WN, WK, DEPTH, kEpiStoreF32>, grid, block, 0, stream, a);

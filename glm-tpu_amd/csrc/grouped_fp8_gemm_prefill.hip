@@ -1321,6 +1321,7 @@ hipError_t launch_prefill_fp8(const GroupedGemmArgs& a, hipStream_t stream) {
   const int64_t R = TALL ? 1 : stripe_run_of(a);
   const int64_t items = (a.n / BN + R - 1) / R * a.max_tiles;
   const int64_t grid = prefill_grid(items);
+  label_grouped_gemm(a, TABLES, a.tile_rows, BN, "_e4m3");
   return launch_kernel(prefill_gemm_fp8_kernel<TABLES, RG, WAVES, EPI>, dim3((unsigned)grid), dim3(64 * WAVES),
                        (size_t)kPrefillLds, stream, a);
 }
@@ -1333,6 +1334,7 @@ hipError_t launch_prefill(const GroupedGemmArgs& a, hipStream_t stream) {
   if (err != hipSuccess) return err;
   const int64_t items = (int64_t)(a.n / BN) * a.max_tiles;  // one stripe per item (a.stripe_run unused)
   const int64_t grid = prefill_grid(items);
+  label_grouped_gemm(a, TABLES, a.tile_rows, BN, "");
   return launch_kernel(prefill_gemm_kernel<TABLES, RG, WAVES, EPI>, dim3((unsigned)grid), dim3(64 * WAVES),
                        (size_t)kPrefillLds, stream, a);
 }

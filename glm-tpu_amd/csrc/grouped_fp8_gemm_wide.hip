@@ -196,6 +196,7 @@ hipError_t launch_wide_shape(const GroupedGemmArgs& a, int epilogue, hipStream_t
   constexpr int BN = WAVES * RG * 16;
   const dim3 grid(a.max_tiles, a.n / BN);
   const dim3 block(64 * WAVES);
+  label_grouped_gemm(a, TABLES, 128, BN, "");
   switch (epilogue) {
     case kEpiStoreF32:
       return launch_kernel(grouped_fp8_gemm_wide_kernel<TABLES, RG, CGMAX, WAVES, kEpiStoreF32>, grid, block, 0, stream, a);

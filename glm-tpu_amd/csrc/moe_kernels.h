@@ -3,6 +3,7 @@
 
 #include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
+#include <rocprofiler-sdk-roctx/roctx.h>
 #include <stdint.h>
 
 #include <atomic>
@@ -35,9 +36,24 @@ struct LaunchEvents {
 };
 LaunchEvents& next_launch_events();  // thread-local; defined in capi.hip
 
+// Profiler name of the next launch on this thread: the reference's kernel
+// names with their shape suffix (glm_tpu/kernels/names.py:1-31, e.g.
+// fp8_routed_projection_s{slots}_t{tables}_k{K}_n{N}_tn{tn}_tk{tk},
+// fp8_grouped_matmul/kernel.py:283).  launch_kernel wraps the launch in a
+// roctx range of that name, which `rocprofv3 --kernel-trace --kernel-rename`
+// reports as the kernel's name, so one profile splits by configuration.
+// The next launch consumes it; an empty label opens no range.  A refused C-ABI
+// call clears it (capi.hip), so no stale name reaches a later launch.
+constexpr int kLabelBytes = 128;
+char* next_launch_label();  // thread-local, kLabelBytes; defined in capi.hip
+void label_next_launch(const char* fmt, ...) __attribute__((format(printf, 1, 2)));
+
 template <typename... KArgs, typename... Args>
 hipError_t launch_kernel(void (*kernel)(KArgs...), dim3 grid, dim3 block, size_t lds, hipStream_t stream,
                          Args&&... args) {
+  char* label = next_launch_label();
+  const bool labelled = label[0] != '\0';
+  if (labelled) roctxRangePushA(label);
   LaunchEvents& ev = next_launch_events();
   if (ev.start != nullptr || ev.stop != nullptr) {
     const LaunchEvents armed = ev;
@@ -47,7 +63,12 @@ hipError_t launch_kernel(void (*kernel)(KArgs...), dim3 grid, dim3 block, size_t
   } else {
     hipLaunchKernelGGL(kernel, grid, block, lds, stream, std::forward<Args>(args)...);
   }
-  return hipGetLastError();
+  const hipError_t err = hipGetLastError();
+  if (labelled) {
+    roctxRangePop();
+    label[0] = '\0';
+  }
+  return err;
 }
 
 // ------------------------------------------------------------------ route plan
@@ -205,7 +226,20 @@ struct GroupedGemmArgs {
   int32_t tile_rows;           // routes per tile of the work list (0: unknown, up to 256)
   int32_t wide_twice;          // the work list names tiles of more than 128 routes twice (RoutePlanArgs)
   int32_t tall;                // prefill kernels: tall stripes (512 weight rows) where N allows them
+  const char* name;            // profiler base name (null: fp8_expert_panel_matmul)
 };
+
+// Profiler name of a grouped-GEMM launch: fp8_routed_projection_s{slots}_t{tables}
+// _k{K}_n{N}_tn{weight rows a workgroup}_tk128 for the routed-projection entry
+// point (the reference's suffix), fp8_expert_panel_matmul{variant}_m{routes}
+// _t{tables}_k{K}_n{N}_tm{routes a tile}_tn{weight rows a work item} otherwise.
+inline void label_grouped_gemm(const GroupedGemmArgs& a, int tables, int tile_rows, int bn, const char* variant) {
+  if (a.name != nullptr)
+    label_next_launch("%s_s%d_t%d_k%d_n%d_tn%d_tk128", a.name, a.rows, tables, a.k, a.n, bn);
+  else
+    label_next_launch("fp8_expert_panel_matmul%s_m%d_t%d_k%d_n%d_tm%d_tn%d", variant, a.rows, tables, a.k, a.n,
+                      tile_rows, bn);
+}
 
 // Kernel shape families chosen by the host from the number of routes per tile.
 enum GemmShape : int {

@@ -512,16 +512,20 @@ hipError_t launch_route_plan(const RoutePlanArgs& a, hipStream_t stream) {
   const size_t lds = sizeof(int) * (size_t)(3 * ep + kPlanWaves + 2) +
                      sizeof(uint16_t) * (size_t)kPlanWaves * ep + (size_t)kPlanWaves * ep;
   const int chunks = route_plan_chunks(a.n, a.top_k);
-  if (a.chunk_hist == nullptr || a.chunk_bad == nullptr || chunks <= 1)
+  if (a.chunk_hist == nullptr || a.chunk_bad == nullptr || chunks <= 1) {
+    label_next_launch("group_prefill_routes_r%d_e%d_tm%d", a.n, a.experts, a.tile_rows);
     return launch_kernel(route_plan_kernel, dim3(1), dim3(kPlanThreads), lds, stream, a);
+  }
   RoutePlanArgs b = a;
   b.chunk = (kPlanChunkRoutes / a.top_k) * a.top_k;
   // the stage timer (if armed) measures the scatter pass: the plan's last kernel
   const LaunchEvents armed = next_launch_events();
   next_launch_events() = LaunchEvents{};
+  label_next_launch("group_prefill_routes_hist_r%d_e%d", a.n, a.experts);
   hipError_t err = launch_kernel(route_hist_kernel, dim3(chunks), dim3(kPlanThreads), 0, stream, b);
   if (err != hipSuccess) return err;
   next_launch_events() = armed;
+  label_next_launch("group_prefill_routes_scatter_r%d_e%d_tm%d", a.n, a.experts, a.tile_rows);
   return launch_kernel(route_scatter_kernel, dim3(chunks), dim3(kPlanThreads), lds, stream, b, chunks, chunks, 1);
 }
 
@@ -562,6 +566,7 @@ hipError_t launch_route_plan_from_logits(const RoutePlanArgs& a, const RouterPas
   const int rows = (int)((r.tokens + kRouterHistTokens - 1) / kRouterHistTokens);
   const LaunchEvents armed = next_launch_events();
   next_launch_events() = LaunchEvents{};
+  label_next_launch("route_glm_noaux_tc_hist_t%lld_e%d_k%d", (long long)r.tokens, r.experts, a.top_k);
   hipError_t err =
       r.experts <= 256
           ? launch_kernel(route_hist_from_logits_kernel<4>, dim3(rows), dim3(64 * kRouterHistTokens), 0, stream, b, r)
@@ -569,17 +574,20 @@ hipError_t launch_route_plan_from_logits(const RoutePlanArgs& a, const RouterPas
                           stream, b, r);
   if (err != hipSuccess) return err;
   next_launch_events() = armed;
+  label_next_launch("group_prefill_routes_scatter_r%d_e%d_tm%d", a.n, a.experts, a.tile_rows);
   return launch_kernel(route_scatter_kernel, dim3(chunks), dim3(kPlanThreads), lds, stream, b, chunks, rows,
                        (int)(ct / kRouterHistTokens));
 }
 
 hipError_t launch_panel_plan(const PanelPlanArgs& a, hipStream_t stream) {
+  label_next_launch("build_expert_panels_r%d_g%d_p%d", a.rows, a.groups, a.panel_rows);
   return launch_kernel(panel_plan_kernel, dim3(1), dim3(kPlanThreads), 0, stream, a);
 }
 
 hipError_t launch_slot_tiles(const int32_t* local_ids, const uint8_t* owned, int32_t slots,
                              int32_t experts, int32_t* tile_expert, int32_t* tile_row,
                              int32_t* tile_live, int32_t* tile_count, hipStream_t stream) {
+  label_next_launch("fp8_routed_projection_plan_s%d", slots);
   return launch_kernel(slot_tiles_kernel, dim3(1), dim3(64), 0, stream, local_ids, owned, slots,
                      experts, tile_expert, tile_row, tile_live, tile_count);
 }

@@ -408,7 +408,8 @@ def _blas_threads(n: int):
 def routed_experts(hidden, route_indices, route_weights, gate_bits, gate_scale, up_bits, up_scale,
                    down_bits, down_scale, route_sum: str = "float32", check_weights: bool = True,
                    drop_unowned: bool = False, activations: str = "bfloat16", workers: int | None = None,
-                   num_experts: int | None = None, expert_offset: int = 0, round_output: bool = True):
+                   num_experts: int | None = None, expert_offset: int = 0, round_output: bool = True,
+                   return_route_max: bool = False):
     """The routed half of the MoE layer, returned as ``(bf16 [T, H] values, valid)``.
 
     ``prefill_moe_from_routes`` (``routed_experts.py:82-117``) on one device
@@ -448,6 +449,11 @@ def routed_experts(hidden, route_indices, route_weights, gate_bits, gate_scale, 
     ``round_output=False`` returns the share's partial before the sum over the
     expert axis: the FP32 route sum, or with ``route_sum="bfloat16"`` that sum
     rounded to bf16 (the decode body's per-owner sum, ``:293-295``).
+
+    ``return_route_max=True`` appends ``max over slots |bf16(down * w)|`` per
+    output element (FP32 ``[T, H]``): the largest bf16-rounded value the
+    element's sum passes through, the scale of a one-ulp rounding difference
+    in any of its routes.
     """
     x = bf16_round(np.asarray(hidden, np.float32))
     ids = np.asarray(route_indices, np.int32)
@@ -514,9 +520,10 @@ def routed_experts(hidden, route_indices, route_weights, gate_bits, gate_scale, 
     total = np.zeros((t, h), np.float32)
     for s in range(k):
         total += per_slot[:, s]
-    if not round_output and route_sum == "float32":
-        return total, valid
-    return bf16_round(total), valid
+    out = total if not round_output and route_sum == "float32" else bf16_round(total)
+    if return_route_max:
+        return out, valid, np.abs(per_slot).max(axis=1)
+    return out, valid
 
 
 def shared_expert(hidden, shared_gate, shared_up, shared_down) -> np.ndarray:
@@ -530,22 +537,34 @@ def shared_expert(hidden, shared_gate, shared_up, shared_down) -> np.ndarray:
 
 def moe_layer(hidden, route_indices, route_weights, gate_bits, gate_scale, up_bits, up_scale,
               down_bits, down_scale, shared_gate, shared_up, shared_down,
-              routed_scaling_factor: float = 2.5, route_sum: str = "float32", decode: bool = False):
+              routed_scaling_factor: float = 2.5, route_sum: str = "float32", decode: bool = False,
+              return_magnitude: bool = False):
     """Whole layer ``bf16(bf16(routed) * bf16(2.5) + shared)`` (``routed_experts.py:125,303-304``).
 
     Returns ``(bf16 [T, H] values, valid)``; ``valid`` also requires a finite
     output (``:126``).  ``decode=True`` is ``moe_grouped_routes``: the
     per-owner bf16 route sum (one rounding of the FP32 sum, as in
     ``routed_experts``), unowned routes dropped, no health checks on the weights.
+
+    ``return_magnitude=True`` appends, per output element, the largest
+    magnitude among the bf16-rounded values it passes through (every route's
+    ``bf16(down * w)`` scaled by 2.5, ``bf16(routed * 2.5)``, the shared
+    expert's output, the output): the scale of a one-ulp rounding difference
+    upstream.
     """
-    routed, valid = routed_experts(hidden, route_indices, route_weights, gate_bits, gate_scale,
-                                   up_bits, up_scale, down_bits, down_scale,
-                                   route_sum="bfloat16" if decode else route_sum,
-                                   check_weights=not decode, drop_unowned=decode)
+    routed, valid, route_max = routed_experts(hidden, route_indices, route_weights, gate_bits, gate_scale,
+                                              up_bits, up_scale, down_bits, down_scale,
+                                              route_sum="bfloat16" if decode else route_sum,
+                                              check_weights=not decode, drop_unowned=decode,
+                                              return_route_max=True)
     shared = shared_expert(hidden, shared_gate, shared_up, shared_down)
     scale = bf16_round(np.float32(routed_scaling_factor))
-    out = bf16_round(bf16_round(routed * scale) + shared)
-    return out, bool(valid and np.all(np.isfinite(out)))
+    scaled = bf16_round(routed * scale)
+    out = bf16_round(scaled + shared)
+    valid = bool(valid and np.all(np.isfinite(out)))
+    if return_magnitude:
+        return out, valid, np.maximum.reduce([route_max * scale, np.abs(scaled), np.abs(shared), np.abs(out)])
+    return out, valid
 
 
 # ----------------------------------------------------------------------------- router

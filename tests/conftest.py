@@ -13,13 +13,24 @@ from pathlib import Path
 import pytest
 
 ROOT = Path(__file__).resolve().parents[1]
-for path in (ROOT, ROOT / "glm-tpu_amd"):
+for path in (ROOT, ROOT / "glm-tpu_amd", ROOT / "tests"):
     if str(path) not in sys.path:
         sys.path.insert(0, str(path))
 
 
 def pytest_configure(config):
     config.addinivalue_line("markers", "gpu: needs an MI355X (gfx950) and the built libglm_moe.so")
+
+
+def pytest_terminal_summary(terminalreporter):
+    """Print every closeness check's measured flips beside its bounds (also under -q)."""
+    import closeness
+
+    lines = closeness.summary_lines()
+    if lines:
+        terminalreporter.section("parity against the oracle")
+        for line in lines:
+            terminalreporter.write_line(line)
 
 
 @pytest.fixture(scope="session")

@@ -16,13 +16,14 @@ import numpy as np
 import pytest
 import torch
 
+import closeness
 from oracle import moe_oracle as O
 
 pytestmark = pytest.mark.gpu
 
 GOLDEN = Path(__file__).resolve().parent / "golden" / "toy_moe.npz"
-MAX_ABS = 2e-2
-MEAN_REL = 5e-3
+MAX_ABS = closeness.MAX_ABS
+MEAN_REL = closeness.MEAN_REL
 TABLE_KEYS = ("gate_bits", "gate_scale", "up_bits", "up_scale", "down_bits", "down_scale")
 
 
@@ -42,46 +43,10 @@ def bf16_bits_of(t):
     return t.cpu().view(torch.int16).numpy().view(np.uint16)
 
 
-FLIP_FRACTION = 2e-3  # at most this share of elements may carry an admitted rounding flip
-FLIP_ULPS = 2         # an admitted flip moves an element by at most this many bf16 ulps
-
-
-def bf16_ulp(values):
-    """One bf16 unit in the last place at |values| (8 significant bits)."""
-    mag = np.maximum(np.abs(np.asarray(values, np.float64)), 2.0**-126)
-    return np.exp2(np.floor(np.log2(mag)) - 7)
-
-
-def assert_moe_close(got, ref, max_abs=MAX_ABS, mean_rel=MEAN_REL):
-    """The north-star tolerance against the oracle's bf16 output: max-abs 2e-2
-    and mean-rel mean|y - y_ref| / mean|y_ref| 5e-3.
-
-    One exception, which no other FP32 summation order can avoid: a route's
-    result passes three bf16 roundings (its down sum, its weighting, the route
-    sum), and an FP32 sum that lands on the other side of a rounding boundary
-    than the oracle's moves the value by one bf16 ulp at that point.  Where
-    bf16 ulps of the output exceed max-abs (|y| >= 2, ulp 2^-6 and up), such
-    flips are admitted: at most FLIP_ULPS ulps each, on at most FLIP_FRACTION of
-    the elements; everywhere else max-abs holds.  (Measured at full prefill
-    size: 98.7 % of elements bit-equal to the oracle, mean-rel 4e-5, one element
-    in 2.3e7 two ulps off at |y| = 2.66; the decode layer's x2.5 output has
-    more elements above |y| = 2, and 2 of its 6144 flipped by one ulp.)
-    Returns (max-abs, mean-rel, flips)."""
-    got = np.asarray(got, np.float64)
-    ref = np.asarray(ref, np.float64)
-    assert np.all(np.isfinite(got)), "non-finite output"
-    diff = np.abs(got - ref)
-    rel = diff.mean() / max(np.abs(ref).mean(), 1e-30)
-    over = diff > max_abs
-    flips = int(over.sum())
-    if flips:
-        ulp = bf16_ulp(ref[over])
-        assert np.all(diff[over] <= FLIP_ULPS * ulp), (
-            f"max-abs {diff.max():.3e} > {max_abs}, beyond {FLIP_ULPS} bf16 ulps at |y| = "
-            f"{np.abs(ref[over]).max():.3f}")
-        assert flips <= max(1, FLIP_FRACTION * diff.size), f"{flips} rounding flips in {diff.size} elements"
-    assert rel <= mean_rel, f"mean-rel {rel:.3e} > {mean_rel}"
-    return diff.max(), rel, flips
+def assert_moe_close(got, ref, **bounds):
+    """The north-star tolerance with the rounding-flip allowance of
+    ``closeness.check`` (recorded and printed in the session summary)."""
+    return closeness.check(got, ref, **bounds)
 
 
 # ----------------------------------------------------------------------------- FP8 decode
@@ -455,14 +420,17 @@ def test_resident_shared_expert_layer(device, tokens, experts, hidden, inter, to
     kw = dict(route_sum="bfloat16", check_weights=False, drop_unowned=True) if decode else {}
     args = (bf16_dev(x, device), dev(ids, device), dev(w, device), *(t[k] for k in TABLE_KEYS))
     got, ok = routed_experts(*args, shared_tables=tuple(shared_dev), **kw)
-    ref, ref_ok = O.moe_layer(x, ids, w, **tables, shared_gate=shared_f32[0], shared_up=shared_f32[1],
-                              shared_down=shared_f32[2], decode=decode)
+    ref, ref_ok, mag = O.moe_layer(x, ids, w, **tables, shared_gate=shared_f32[0], shared_up=shared_f32[1],
+                                   shared_down=shared_f32[2], decode=decode, return_magnitude=True)
     assert bool(ok) == ref_ok
-    print(cfg, "vs oracle:", assert_moe_close(host_f32(got), ref))
+    print(cfg, "vs oracle:", assert_moe_close(host_f32(got), ref, magnitude=mag, flip_ulps=closeness.LAYER_FLIP_ULPS,
+                                              max_flips=closeness.layer_max_flips(ref.size)))
     # the same layer with the shared expert on hipBLASLt: equal up to FP32 summation order
     shared = _shared_swiglu(args[0], *shared_dev)
     other, _ = routed_experts(*args, shared=shared, **kw)
-    print("vs hipBLASLt shared expert:", assert_moe_close(host_f32(got), host_f32(other)))
+    print("vs hipBLASLt shared expert:", assert_moe_close(host_f32(got), host_f32(other), magnitude=mag,
+                                                          label="vs hipBLASLt", flip_ulps=closeness.LAYER_FLIP_ULPS,
+                                                          max_flips=closeness.layer_max_flips(ref.size)))
     again, _ = routed_experts(*args, shared_tables=tuple(shared_dev), **kw)
     np.testing.assert_array_equal(bf16_bits_of(again), bf16_bits_of(got))  # deterministic
 
@@ -746,9 +714,9 @@ def test_decode_production_shape_matches_oracle(device, production_tables, name)
     t = production_tables
     out, ok = routed_experts(bf16_dev(x, device), dev(ids, device), dev(w, device), *(t[k] for k in TABLE_KEYS))
     host, local_ids = _subproblem(t, ids)
-    ref, _ = O.routed_experts(x, local_ids, w, **host)
+    ref, _, mag = O.routed_experts(x, local_ids, w, **host, return_route_max=True)
     assert bool(ok)
-    print(name, assert_moe_close(host_f32(out), ref))
+    print(name, assert_moe_close(host_f32(out), ref, magnitude=mag))
     again, _ = routed_experts(bf16_dev(x, device), dev(ids, device), dev(w, device), *(t[k] for k in TABLE_KEYS))
     np.testing.assert_array_equal(bf16_bits_of(again), bf16_bits_of(out))  # deterministic
 
@@ -824,8 +792,67 @@ def test_prefill_production_shape_every_tile(device, production_tables, name):
     rows = covering_rows(ids, cfg.experts)
     assert set(np.unique(ids[rows])) == set(np.unique(ids))  # every expert with routes
     host, local_ids = _subproblem(t, ids[rows])
-    ref, _ = O.routed_experts(x[rows], local_ids, w[rows], **host)
-    print(name, f"{len(rows)} of {cfg.tokens} rows:", assert_moe_close(full[rows], ref))
+    ref, _, mag = O.routed_experts(x[rows], local_ids, w[rows], **host, return_route_max=True)
+    # one flip of 2 ulps measured at T=8192 Zipf (in 2.3e7 elements): a route's
+    # down value flipped by one ulp moves bf16(down * w) by 2 ulps of it where
+    # w < 1 takes the product into the next lower binade
+    print(name, f"{len(rows)} of {cfg.tokens} rows:", assert_moe_close(full[rows], ref, magnitude=mag, flip_ulps=2))
+
+
+def _shared_expert_tables(cfg, seed):
+    """bf16-valued shared-expert weights [I, H], [I, H], [H, I] (I = the routed
+    experts' intermediate size, GLM-5's single shared expert)."""
+    rng = np.random.default_rng(seed)
+    return [O.bf16_round((rng.standard_normal(shape) * std).astype(np.float32))
+            for shape, std in (((cfg.intermediate, cfg.hidden), cfg.hidden ** -0.5),
+                               ((cfg.intermediate, cfg.hidden), cfg.hidden ** -0.5),
+                               ((cfg.hidden, cfg.intermediate), 2 * cfg.intermediate ** -0.5))]
+
+
+@pytest.mark.parametrize("name", ["prefill_t2048", "prefill_t8192_zipf"])
+def test_prefill_layer_production_size_matches_oracle(device, production_tables, name):
+    """The whole prefill layer body at the BASELINE prefill configs, as served:
+    ``prefill_moe_from_routes`` (route plan, grouped GEMMs, the bf16 shared
+    expert on hipBLASLt, ``bf16(bf16(routed x bf16(2.5)) + shared)`` fused into
+    the route combine, the health bit; routed_experts.py:27-128) against the
+    oracle's ``moe_layer`` (tests/reference/moe.py:78-99) on the rows that reach
+    every expert, every 128 routes and every 16-route column group.  The whole
+    output is finite; a duplicate id or a NaN weight clears health."""
+    from glm_moe import synthetic as S
+    from glm_moe.contracts import single_gpu_contract
+    from glm_moe.layers.moe.routed_experts import prefill_moe_from_routes
+
+    cfg = S.CONFIGS[name]
+    contract = single_gpu_contract(hidden_size=cfg.hidden, intermediate_size=cfg.intermediate,
+                                   num_experts=cfg.experts, top_k=cfg.top_k)
+    shared_f32 = _shared_expert_tables(cfg, 41)
+    shared_dev = tuple(bf16_dev(a, device) for a in shared_f32)
+    x = S.hidden_states(cfg, 21)
+    ids, w = S.routes(cfg, 21)
+    t = production_tables
+    tables = tuple(t[k] for k in TABLE_KEYS)
+    xs = bf16_dev(x, device)
+    out, ok = prefill_moe_from_routes(xs, dev(ids, device), dev(w, device), *tables, *shared_dev, contract=contract)
+    assert bool(ok)
+    full = host_f32(out)
+    assert np.all(np.isfinite(full))
+    rows = covering_rows(ids, cfg.experts)
+    host, local_ids = _subproblem(t, ids[rows])
+    ref, ref_ok, mag = O.moe_layer(x[rows], local_ids, w[rows], *(host[k] for k in TABLE_KEYS), *shared_f32,
+                                   return_magnitude=True)
+    assert ref_ok
+    print(name, f"layer, {len(rows)} of {cfg.tokens} rows:",
+          assert_moe_close(full[rows], ref, magnitude=mag, flip_ulps=closeness.LAYER_FLIP_ULPS,
+                           max_flips=closeness.layer_max_flips(ref.size)))
+
+    dup = ids.copy()
+    dup[cfg.tokens // 2, 1] = dup[cfg.tokens // 2, 0]
+    _, ok = prefill_moe_from_routes(xs, dev(dup, device), dev(w, device), *tables, *shared_dev, contract=contract)
+    assert not bool(ok)
+    nan = w.copy()
+    nan[cfg.tokens - 1, 0] = float("nan")
+    _, ok = prefill_moe_from_routes(xs, dev(ids, device), dev(nan, device), *tables, *shared_dev, contract=contract)
+    assert not bool(ok)
 
 
 @pytest.mark.parametrize("tokens,experts,top_k,zipf", [(1024, 16, 8, 1.2), (640, 32, 8, 0.0)])
@@ -984,11 +1011,7 @@ def test_decode_headline_layer_matches_oracle(device, production_tables):
     cfg = S.CONFIGS["decode_t1"]
     contract = single_gpu_contract(hidden_size=cfg.hidden, intermediate_size=cfg.intermediate,
                                    num_experts=cfg.experts, top_k=cfg.top_k)
-    rng = np.random.default_rng(31)
-    shared_f32 = [O.bf16_round((rng.standard_normal(shape) * std).astype(np.float32))
-                  for shape, std in (((cfg.intermediate, cfg.hidden), cfg.hidden ** -0.5),
-                                     ((cfg.intermediate, cfg.hidden), cfg.hidden ** -0.5),
-                                     ((cfg.hidden, cfg.intermediate), 2 * cfg.intermediate ** -0.5))]
+    shared_f32 = _shared_expert_tables(cfg, 31)
     shared_dev = tuple(bf16_dev(a, device) for a in shared_f32)
     t = production_tables
     for seed in (8, 9, 10):
@@ -997,8 +1020,11 @@ def test_decode_headline_layer_matches_oracle(device, production_tables):
         got = moe_grouped_routes(bf16_dev(x, device), dev(ids, device), dev(w, device), *(t[k] for k in TABLE_KEYS),
                                  contract=contract, shared_bf16=shared_dev)
         host, local_ids = _subproblem(t, ids)
-        ref, _ = O.moe_layer(x, local_ids, w, *(host[k] for k in TABLE_KEYS), *shared_f32, decode=True)
-        print("decode headline layer", seed, assert_moe_close(host_f32(got), ref))
+        ref, _, mag = O.moe_layer(x, local_ids, w, *(host[k] for k in TABLE_KEYS), *shared_f32, decode=True,
+                                  return_magnitude=True)
+        print("decode headline layer", seed,
+              assert_moe_close(host_f32(got), ref, magnitude=mag, label=f"seed {seed}",
+                               flip_ulps=closeness.LAYER_FLIP_ULPS, max_flips=closeness.layer_max_flips(ref.size)))
 
 
 # ----------------------------------------------------------------------------- native FP8 mode
@@ -1010,20 +1036,21 @@ FP8_ERROR_BOUND = 5e-2  # mean-rel against the bf16 reference numerics (e4m3 act
 # but not max-abs 2e-2: its activations are re-quantised to e4m3 per 128-wide
 # block, so a one-ulp bf16 difference in a SwiGLU value (the FP32 sums of the
 # gate/up projections rounding the other way) can move its block's amax, hence
-# the block scale, and re-round all 128 e4m3 values of the block.  Measured at
-# full prefill size: mean-rel 1.3e-3, max-abs 0.039, in 47 of 1114 rows.
-FP8_MAX_ABS = 6.25e-2
+# the block scale, and re-round all 128 e4m3 values of the block, which moves
+# the route's whole down row.  Measured at full prefill size: T=8192 Zipf
+# mean-rel 1.3e-3, max-abs 0.039, 445 of 6.8e6 elements (6.5e-5) beyond 2e-2;
+# T=2048 none.
+FP8_MAX_ABS = 5e-2
 
 
-def assert_fp8_close(got, ref):
-    got = np.asarray(got, np.float64)
-    ref = np.asarray(ref, np.float64)
-    assert np.all(np.isfinite(got)), "non-finite output"
-    diff = np.abs(got - ref)
-    rel = diff.mean() / max(np.abs(ref).mean(), 1e-30)
-    assert diff.max() <= FP8_MAX_ABS, f"max-abs {diff.max():.3e} > {FP8_MAX_ABS}"
-    assert rel <= MEAN_REL, f"mean-rel {rel:.3e} > {MEAN_REL}"
-    return diff.max(), rel
+FP8_OVER_FRACTION = 2e-4  # elements beyond max-abs 2e-2 (measured 6.5e-5; a re-quantised block moves a route row)
+
+
+def assert_fp8_close(got, ref, label="fp8 mode vs its oracle"):
+    c = closeness.check(got, ref, label=label, flip_ulps=np.inf,
+                        max_flips=int(FP8_OVER_FRACTION * np.size(ref)))
+    assert c.max_abs <= FP8_MAX_ABS, f"max-abs {c.max_abs:.3e} > {FP8_MAX_ABS}"
+    return c
 
 
 def test_fp8_mode_matches_its_oracle_and_reports_its_error(device):

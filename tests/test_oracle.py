@@ -7,6 +7,8 @@ term, a wrong index or sign, a transposed operand) fails it.
 
 from __future__ import annotations
 
+import math
+
 import numpy as np
 import pytest
 import torch
@@ -240,30 +242,54 @@ def test_routed_projection_clips_ids_and_zeroes_unowned_slots():
 
 
 # ----------------------------------------------------------------------------- SwiGLU and routed experts
+def _swiglu_torch_stepwise(g, u):
+    """tests/reference/linear.py:71-73 in torch bf16, one op at a time: each
+    bf16 op computes in FP32 and rounds once."""
+    gb = torch.from_numpy(np.asarray(g, np.float32)).to(torch.bfloat16)
+    ub = torch.from_numpy(np.asarray(u, np.float32)).to(torch.bfloat16)
+    s = torch.sigmoid(gb)
+    gs = gb * s
+    return (gs * ub).float().numpy()
+
+
 def test_swiglu_rounds_after_every_op():
     g = O.bf16_round(np.linspace(-8, 8, 4097).astype(np.float32))
     u = O.bf16_round(np.float32(1.0) + np.zeros_like(g))
     np.testing.assert_array_equal(O.swiglu_bf16(g, np.zeros_like(g)), 0)
-    s = torch.sigmoid(torch.from_numpy(g).to(torch.bfloat16))  # torch: f32 math, one rounding
-    expected = (torch.from_numpy(g).to(torch.bfloat16) * s).float().numpy()
-    np.testing.assert_array_equal(O.swiglu_bf16(g, u), expected)
+    np.testing.assert_array_equal(O.swiglu_bf16(g, u), _swiglu_torch_stepwise(g, u))
+    # u != 1: the last product's rounding (and the rounding of g * sigmoid(g) before it)
+    rng = np.random.default_rng(4)
+    g = O.bf16_round((rng.standard_normal(1 << 16) * 4).astype(np.float32))
+    u = O.bf16_round((rng.standard_normal(1 << 16) * 3).astype(np.float32))
+    want = _swiglu_torch_stepwise(g, u)
+    np.testing.assert_array_equal(O.swiglu_bf16(g, u), want)
+    # planted mistakes the comparison must catch: g * sigmoid(g) not rounded
+    # before the product with u, and the sigmoid not rounded before g * s
+    s = O.bf16_round(O.sigmoid_f32(g))
+    assert not np.array_equal(O.bf16_round(g * s * u), want)
+    assert not np.array_equal(O.bf16_round(O.bf16_round(g * O.sigmoid_f32(g)) * u), want)
 
 
-def _fp64_routed(x, ids, w, tables, route_sum_scale=1.0):
-    """tests/reference/independent.py:257-287 form: FP64 everywhere after the bf16 weight decode."""
+def _fp64_routed_slots(x, ids, w, tables, route_sum_scale=1.0):
+    """tests/reference/independent.py:257-287 form: FP64 everywhere after the
+    bf16 weight decode; every route's weighted down row, ``[T, k, H]``."""
     def dq(bits, scales):
         v = torch.from_numpy(bits).view(torch.float8_e4m3fn).double().numpy()
         ex = np.repeat(np.repeat(scales.astype(np.float64), 128, -2), 128, -1)
         return torch.from_numpy((v * ex).astype(np.float32)).to(torch.bfloat16).double().numpy()
-    out = np.zeros((x.shape[0], x.shape[1]))
+    out = np.zeros((ids.shape[0], ids.shape[1], x.shape[1]))
     for t in range(ids.shape[0]):
         for s in range(ids.shape[1]):
             e = ids[t, s]
             gate = dq(tables["gate_bits"][e], tables["gate_scale"][e]) @ x[t]
             up = dq(tables["up_bits"][e], tables["up_scale"][e]) @ x[t]
             act = gate / (1 + np.exp(-gate)) * up
-            out[t] += w[t, s] * route_sum_scale * (dq(tables["down_bits"][e], tables["down_scale"][e]) @ act)
+            out[t, s] = w[t, s] * route_sum_scale * (dq(tables["down_bits"][e], tables["down_scale"][e]) @ act)
     return out
+
+
+def _fp64_routed(x, ids, w, tables, route_sum_scale=1.0):
+    return _fp64_routed_slots(x, ids, w, tables, route_sum_scale).sum(axis=1)
 
 
 def test_routed_experts_matches_fp64_restatement_and_catches_planted_mistakes():
@@ -417,6 +443,16 @@ def test_moe_layer_matches_fp64_restatement_and_catches_planted_mistakes():
     # the decode body (unowned dropped, per-owner bf16 sum) on all-owned routes: the same bits
     dec, _ = O.moe_layer(x, ids, w, *tables.values(), *shared, decode=True)
     np.testing.assert_array_equal(dec, got)
+    # the magnitude the parity checks scale rounding flips by: the same output,
+    # and per element at least |output|, |2.5 x routed|, |shared| and every
+    # route's 2.5 x |bf16(down * w)| (FP64 restatement, so within its tolerance)
+    same, _, mag = O.moe_layer(x, ids, w, *tables.values(), *shared, return_magnitude=True)
+    np.testing.assert_array_equal(same, got)
+    assert np.all(mag >= np.abs(got))
+    assert np.all(mag >= 2.5 * np.abs(routed) - bound) and np.all(mag >= np.abs(shared_out) - bound)
+    _, _, route_max = O.routed_experts(x, ids, w, **tables, return_route_max=True)
+    per_route = np.abs(_fp64_routed_slots(x, ids, w, tables)).max(axis=1)
+    assert np.abs(route_max - per_route).max() <= 0.015 * per_route.max()
 
 
 # ----------------------------------------------------------------------------- router
@@ -437,7 +473,93 @@ def test_router_ties_choose_lowest_expert_ids():
     np.testing.assert_array_equal(w, np.full((1, 8), 0.125, np.float32))
 
 
+def _brute_force_route(logits, bias, top_k):
+    """An independent restatement of router.py:20-55 by brute force: each score
+    is the FP64 logistic rounded to FP32, the biased score its FP32 sum with the
+    bias, the selection the top_k largest (biased score, -id) pairs of a full
+    Python sort (ties to the lowest id), and the weights FP64 ratios of the
+    chosen unbiased scores.  Returns ids, weights and, per token, the gap between
+    the k-th and (k+1)-th biased scores (where a last-bit sigmoid difference
+    could swap the selection)."""
+    ids, weights, gaps = [], [], []
+    for row in np.asarray(logits, np.float64):
+        scores = [np.float32(1.0 / (1.0 + math.exp(-v))) for v in row]
+        biased = [np.float32(sc + np.float32(b)) for sc, b in zip(scores, bias)]
+        pairs = sorted(((float(v), -e) for e, v in enumerate(biased)), reverse=True)
+        chosen = [-e for _, e in pairs[:top_k]]
+        total = math.fsum(float(scores[e]) for e in chosen)
+        ids.append(chosen)
+        weights.append([float(scores[e]) / total for e in chosen])
+        gaps.append(pairs[top_k - 1][0] - pairs[top_k][0] if top_k < len(pairs) else np.inf)
+    return np.array(ids), np.array(weights), np.array(gaps)
+
+
+def _router_agrees(got, want, gaps):
+    """Ids equal wherever the selection is decided by more than 1e-6; weights
+    within 4e-7 relative (a few FP32 ulps)."""
+    idx, w = got
+    ref_idx, ref_w, _ = want
+    decided = gaps > 1e-6
+    return bool(np.array_equal(idx[decided], ref_idx[decided])
+                and np.allclose(w[decided], ref_w[decided], rtol=4e-7, atol=0))
+
+
+def test_sigmoid_is_the_fp32_logistic_within_four_ulps():
+    """FP32 1 / (1 + exp(-x)) against the FP64 logistic: within 4 FP32 ulps
+    (3.2 measured, at x < 0 where 1 + exp(-x) rounds), within 2 for x >= 0 (1.5);
+    XLA's own last-bit rounding is not pinned (no JAX here)."""
+    x = np.linspace(-30, 30, 600001).astype(np.float32)
+    got = O.sigmoid_f32(x).astype(np.float64)
+    exact = 1.0 / (1.0 + np.exp(-x.astype(np.float64)))
+    ulps = np.abs(got - exact) / np.spacing(exact.astype(np.float32)).astype(np.float64)
+    assert ulps.max() <= 4
+    assert ulps[x >= 0].max() <= 2
+
+
+@pytest.mark.parametrize("experts,top_k,zipf,biased", [(16, 4, 0.0, False), (64, 8, 0.0, True), (256, 8, 1.2, True)])
+def test_router_matches_brute_force_and_catches_planted_mistakes(experts, top_k, zipf, biased):
+    """The oracle router against the brute force above on seeded logits, and
+    three mistakes planted in copies of the oracle that the comparison must
+    catch: weights from the biased scores, selection on the unbiased scores,
+    and the selection order without the bias's effect on ties."""
+    from glm_moe import synthetic as S
+
+    cfg = S.MoeConfig("router", 96, experts, 128, 128, top_k, zipf)
+    logits = S.router_logits(cfg, 3)
+    rng = np.random.default_rng(experts)
+    bias = (rng.standard_normal(experts) * 0.05).astype(np.float32) if biased else np.zeros(experts, np.float32)
+    want = _brute_force_route(logits, bias, top_k)
+    assert np.mean(want[2] > 1e-6) > 0.95
+    got = O.route_glm_noaux_tc_logits(logits, bias, top_k)
+    assert _router_agrees(got, want, want[2])
+    if biased:
+        # planted: the weights normalise the biased scores
+        scores = O.sigmoid_f32(logits)
+        b = (scores + bias[None, :]).astype(np.float32)
+        chosen = np.take_along_axis(b, got[0], axis=-1)
+        assert not _router_agrees((got[0], chosen / chosen.sum(-1, keepdims=True)), want, want[2])
+        # planted: the selection ignores the bias
+        assert not _router_agrees(O.route_glm_noaux_tc_logits(logits, np.zeros_like(bias), top_k), want, want[2])
+
+
+def test_router_ties_brute_force_and_planted_highest_id():
+    """Exact ties (integer logits, zero bias): the brute force and the oracle take
+    the lowest ids; a copy of the oracle that breaks ties to the highest id
+    (run on the experts in reverse order) is caught."""
+    rng = np.random.default_rng(11)
+    logits = rng.integers(-2, 3, (64, 32)).astype(np.float32)
+    bias = np.zeros(32, np.float32)
+    want = _brute_force_route(logits, bias, 6)
+    got = O.route_glm_noaux_tc_logits(logits, bias, 6)
+    np.testing.assert_array_equal(got[0], want[0])
+    np.testing.assert_allclose(got[1], want[1], rtol=4e-7, atol=0)
+    rev_idx, rev_w = O.route_glm_noaux_tc_logits(logits[:, ::-1].copy(), bias, 6)
+    assert not np.array_equal(31 - rev_idx, want[0])
+
+
 def test_synthetic_router_agrees_with_oracle_router():
+    """The bench's input generator routes as the oracle does (both are checked
+    against the brute force above, not against each other alone)."""
     from glm_moe import synthetic as S
 
     for name in ("toy", "decode_t4", "prefill_t8192_zipf"):
@@ -449,6 +571,8 @@ def test_synthetic_router_agrees_with_oracle_router():
         b = O.route_glm_noaux_tc_logits(logits, np.zeros(cfg.experts, np.float32), cfg.top_k)
         np.testing.assert_array_equal(a[0], b[0])
         np.testing.assert_array_equal(a[1], b[1])
+        want = _brute_force_route(logits, np.zeros(cfg.experts, np.float32), cfg.top_k)
+        assert _router_agrees(a, want, want[2])
 
 
 # ----------------------------------------------------------------------------- native FP8 mode (no reference counterpart)
