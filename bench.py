@@ -54,7 +54,7 @@ def parse_args():
     p.add_argument("--warmup", type=int, default=10)
     p.add_argument("--config", default="decode_t1")
     p.add_argument("--secondary",
-                   default="decode_t4,batch_t64,prefill_t2048,prefill_t8192_zipf,prefill_t2048:fp8,"
+                   default="decode_t4,batch_t64,prefill_t128,prefill_t2048,prefill_t8192_zipf,prefill_t2048:fp8,"
                            "prefill_t8192_zipf:fp8,"
                            "prefill_t2048:share8",
                    help="comma-separated extra configs measured after the headline ('' for none); a ':fp8' "
@@ -273,10 +273,10 @@ def full_layer(work, steps, warmup):
     out = torch.empty((cfg.tokens, cfg.hidden), dtype=torch.bfloat16, device=device)
     n_rot = len(work.inputs)
 
-    # one row (the decode body): the shared expert inside the decode kernels; 2-8
-    # rows: the few-row kernels; more: hipBLASLt (each reads the shared weights once)
-    resident = work.activations == "bfloat16" and cfg.tokens == 1 and uses_decode_kernels(
-        1, cfg.top_k, cfg.hidden, cfg.intermediate)
+    # up to 8 rows on the decode kernels: the shared expert inside them (one row: the
+    # decode body); more: hipBLASLt (each reads the shared weights once)
+    resident = work.activations == "bfloat16" and cfg.tokens <= 8 and uses_decode_kernels(
+        cfg.tokens, cfg.top_k, cfg.hidden, cfg.intermediate)
 
     def layer(i):
         x, ids, w = work.inputs[i % n_rot]
@@ -290,7 +290,8 @@ def full_layer(work, steps, warmup):
     ms, _ = graph_time(layer, steps, warmup)
     shared_bytes = 3 * inter_shared * cfg.hidden * 2
     if resident:
-        how = "shared expert inside the two decode kernels (glm_moe_moe_layer_resident)"
+        how = ("shared expert inside the two decode kernels (glm_moe_moe_layer_resident"
+               + (")" if cfg.tokens == 1 else "; routes grouped by expert, shared rows streamed once per token group)"))
     elif shared_expert_rows_fit(cfg.tokens, cfg.hidden, inter_shared):
         how = "shared expert on the few-row kernels (glm_moe_shared_expert_rows), epilogue fused (glm_moe_moe_layer)"
     else:
@@ -387,53 +388,75 @@ def summarize(work, ms, stages, order):
         "layer_tflops": float(work.flops["total"] / (ms * 1e-3) / 1e12),
         "gate_up_tflops": float(work.flops["gate_up"] / (gate_up_ms.mean() * 1e-3) / 1e12),
         "gate_up_bytes": float(bytes_gu.mean()),
+        "gate_up_flops": float(work.flops["gate_up"]),
         "layer_bytes": float(bytes_total.mean()),
         "distinct_experts": float(np.mean([len(np.unique(work.host[i][1])) for i in order])),
     }
 
 
 DECODE_PATH_MAX_ROUTES = 64  # routes handled by the two decode GEMV kernels (libglm_moe)
-
-# HBM bytes per launch of the dominant kernel, measured with rocprofv3 --pmc
-# (FETCH_SIZE + WRITE_SIZE per dispatch, FETCH_SIZE x2 and WRITE_SIZE x1 by the
-# 1 GiB copy calibration of `bench.py --copy-calibration`); the command and the
-# raw counter summary are in the named profile.
-MEASURED_TRAFFIC = {
-    ("decode_t1", "decode_gate_up_kernel"): {"bytes": 201.80e6, "source": "profiles/decode_t1_hbm_traffic.md"},
-    ("prefill_t2048", "prefill_gemm_kernel"): {"bytes": 6700.1e6, "source": "profiles/prefill_t2048_hbm_traffic.md"},
-}
+PROFILES = ROOT / "profiles"
 
 
-def dominant_roofline(cfg, head):
+def measured_traffic():
+    """HBM bytes per launch of each config's gate/up kernel, read from the
+    profiles/*_hbm_traffic.md summaries: their lines
+    ``bench-traffic: <config[:mode]> <kernel> <bytes>`` hold the rocprofv3 --pmc
+    FETCH_SIZE + WRITE_SIZE per dispatch (scaled by the 1 GiB copy calibration
+    of ``bench.py --copy-calibration``), the figure the summary's table derives."""
+    found = {}
+    for path in sorted(PROFILES.glob("*_hbm_traffic.md")) if PROFILES.is_dir() else []:
+        for line in path.read_text().splitlines():
+            if line.startswith("bench-traffic:"):
+                _, name, kernel, nbytes = line.split()
+                found[name] = {"bytes": float(nbytes), "kernel": kernel, "source": f"profiles/{path.name}"}
+    return found
+
+
+def dominant_roofline(cfg, s, mode=""):
     """Roofline of the stage that dominates the layer: the gate/up projection.
 
-    Decode shapes (at most 64 routes) run the decode GEMV gate/up kernel and are
-    bounded by HBM: achieved = its algorithmic bytes (the selected experts'
-    gate and up e4m3 bytes and scales, the hidden rows and the activations it
-    writes) / its kernel time.  Larger shapes run the grouped GEMM gate/up
-    kernel: achieved = its algorithmic flops / its kernel time against the bf16
-    MFMA peak.  Kernel times come from HIP events the kernel records at its own
-    start and end on the launch stream.
+    The bound follows the kernel's arithmetic intensity (algorithmic flops per
+    algorithmic byte) against the ridge point of the MFMA peak it computes on
+    (bf16, or fp8 in the native FP8 mode) over the 8 TB/s HBM peak: below the
+    ridge it is HBM-bound and achieved = its algorithmic bytes (the selected
+    experts' gate and up e4m3 bytes and scales, the token rows read and the
+    activations written) / its kernel time; above it, achieved = its
+    algorithmic flops / its kernel time against the MFMA peak.  Kernel times
+    come from HIP events the kernel records at its own start and end on the
+    launch stream.  ``traffic`` is the measured HBM bytes per launch of that
+    config's profile summary (null where there is none).
     """
-    gate_up_us = head["stage_us"]["gate_up"]
+    gate_up_us = s["stage_us"]["gate_up"]
     decode_path = cfg.tokens * cfg.top_k <= DECODE_PATH_MAX_ROUTES
+    fp8 = mode == "fp8"
+    peak_tflops = FP8_PEAK_TFLOPS if fp8 else BF16_PEAK_TFLOPS
+    ridge = peak_tflops * 1e12 / (HBM_PEAK_GBS * 1e9)
+    intensity = s["gate_up_flops"] / s["gate_up_bytes"]
     if decode_path:
-        kernel = "decode_gate_up_kernel"
-        achieved = head["gate_up_bytes"] / (gate_up_us * 1e-6) / 1e9
+        kernel = "decode_gate_up_kernel" if cfg.tokens == 1 else "decode_gate_up_multi_kernel"
+    else:
+        kernel = "prefill_gemm_fp8_kernel" if fp8 else "prefill_gemm_kernel"
+    if decode_path or intensity < ridge:
+        achieved = s["gate_up_bytes"] / (gate_up_us * 1e-6) / 1e9
         line = {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": achieved / HBM_PEAK_GBS}
     else:
-        kernel = "prefill_gemm_kernel"
-        achieved = head["gate_up_tflops"]
-        line = {"bound": "mfma", "achieved": achieved, "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
-                "frac": achieved / BF16_PEAK_TFLOPS}
-    measured = MEASURED_TRAFFIC.get((cfg.name, kernel))
+        achieved = s["gate_up_tflops"]
+        line = {"bound": "mfma", "achieved": achieved, "peak": peak_tflops, "unit": "TFLOP/s",
+                "frac": achieved / peak_tflops}
+    measured = measured_traffic().get(cfg.name + (":" + mode if mode else ""))
     line["traffic"] = measured["bytes"] if measured else None
     line["kernel"] = kernel
     line["kernel_us"] = gate_up_us
-    line["algorithmic_bytes"] = head["gate_up_bytes"]
+    line["algorithmic_bytes"] = s["gate_up_bytes"]
+    line["algorithmic_flops"] = s["gate_up_flops"]
+    line["arithmetic_intensity"] = intensity
+    line["ridge"] = ridge
+    line["mfma_frac"] = s["gate_up_tflops"] / peak_tflops
     if measured:
         line["traffic_source"] = measured["source"]
+        line["traffic_over_algorithmic"] = measured["bytes"] / s["gate_up_bytes"]
     return line
 
 
@@ -486,7 +509,9 @@ def cpu_baseline(work, device):
     return {
         "value": per_layer_us,
         "unit": "us/layer",
-        "cores": int(blas_threads),
+        "cores": len(os.sched_getaffinity(0)),
+        "threads": int(blas_threads),
+        "extrapolated": sample_tokens < tokens,
         "kind": "port",
         "sample": (f"numpy oracle (oracle/moe_oracle.py) on {sample_tokens} of {tokens} tokens of routing seed "
                    f"{1000}, {len(used)} experts decoded per run, median of {len(times)} runs; elementwise "
@@ -540,7 +565,10 @@ def cpu_baseline_sampled(work, device):
     return {
         "value": est * 1e6,
         "unit": "us/layer",
-        "cores": int(workers),
+        "cores": len(os.sched_getaffinity(0)),
+        "threads": int(workers),
+        "extrapolated": True,
+        "extrapolation": f"measured on {len(pick)} of {len(used)} experts, scaled to all (value is an estimate)",
         "kind": "port",
         "sample": (f"numpy oracle (oracle/moe_oracle.py) on routing seed 1000: fixed part (grouping, restore, "
                    f"slot sum over all {ids.size} routes) {fixed:.2f} s, plus {len(pick)} of {len(used)} used "
@@ -610,6 +638,7 @@ def measure_secondary(scfg, tables, device, activations, mode, steps, cpu=True):
     s["us_per_layer_eager"] = sms_eager * 1e3
     s["hbm_frac"] = s["layer_hbm_gbs"] / HBM_PEAK_GBS
     s["bf16_mfma_frac"] = s["layer_tflops"] / BF16_PEAK_TFLOPS
+    s["roofline"] = dominant_roofline(scfg, s, mode)
     with_full_layer(s, swork, steps)
     if mode != "fp8":
         with_router(s, scfg, device)

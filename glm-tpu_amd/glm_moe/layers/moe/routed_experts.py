@@ -515,6 +515,7 @@ def _shared_swiglu(hidden: torch.Tensor, gate: torch.Tensor, up: torch.Tensor, d
 
 
 SHARED_ROWS_MAX = 8  # rows the few-row shared-expert kernels take (glm_moe_shared_expert_rows)
+RESIDENT_ROWS_MAX = 8  # rows whose layer runs the shared expert inside the decode kernels
 
 
 def shared_expert_rows_fit(tokens: int, hidden: int, intermediate: int) -> bool:
@@ -648,9 +649,11 @@ def prefill_moe_from_routes(
         out = moe_layer_epilogue(routed, _shared_expert(hidden_local, *tables), valid,
                                  routed_scale=contract.routed_scaling_factor)
         return out, valid
-    if hidden_local.shape[0] == 1 and uses_decode_kernels(1, contract.top_k, h, inter):
-        # one row: the shared expert runs inside the two decode kernels (with more
-        # rows they would stream its weights once per row)
+    rows = hidden_local.shape[0]
+    if rows <= RESIDENT_ROWS_MAX and uses_decode_kernels(rows, contract.top_k, h, inter):
+        # up to 8 rows on the decode kernels: the shared expert runs inside the same
+        # two launches (its weights streamed once per group of up to 4 rows for
+        # gate/up, once for down)
         shared_kw = {"shared_tables": tuple(t.contiguous() for t in tables)}
     else:
         shared_kw = {"shared": _shared_expert(hidden_local, *tables)}

@@ -46,6 +46,8 @@ CONFIGS: dict[str, MoeConfig] = {
     "decode_t4": MoeConfig("decode_t4", 4, 256, 6144, 2048, 8),
     # 64 concurrent chats: 512 routes over ~218 experts, past the decode kernels
     "batch_t64": MoeConfig("batch_t64", 64, 256, 6144, 2048, 8),
+    # the reference engine's prefill block (llm_engine.py:56-62): 128 rows, 1,024 routes
+    "prefill_t128": MoeConfig("prefill_t128", 128, 256, 6144, 2048, 8),
     "prefill_t2048": MoeConfig("prefill_t2048", 2048, 256, 6144, 2048, 8),
     "prefill_t8192_zipf": MoeConfig("prefill_t8192_zipf", 8192, 256, 6144, 2048, 8, zipf=1.2),
 }

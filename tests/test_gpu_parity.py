@@ -403,6 +403,9 @@ def test_fused_layer_nonfinite_output_clears_health(device, tokens, top_k):
     (3, 16, 512, 256, 4, False),    # the prefill body on few rows: FP32 sum
     (8, 32, 768, 384, 8, False),    # 64 routes, the decode kernels' limit
     (2, 8, 6144, 2048, 4, True),    # production hidden / intermediate sizes
+    (5, 16, 512, 256, 8, False),    # two shared token groups (4 + 1 tokens)
+    (8, 8, 512, 256, 8, True),      # every token selects every expert: units of two routes, two shared groups
+    (4, 256, 6144, 2048, 8, True),  # the batched decode layer (decode_t4 shape)
 ])
 def test_resident_shared_expert_layer(device, tokens, experts, hidden, inter, top_k, decode):
     from glm_moe.layers.moe.routed_experts import _shared_swiglu, routed_experts, uses_decode_kernels
@@ -473,6 +476,8 @@ def _small_case(tokens, experts, hidden, inter, top_k, zipf, seed):
     (512, 256, 768, 256, 8, 0.0),   # prefill path over 256 experts of ~16 routes (one tile each)
     (1536, 256, 768, 256, 8, 1.2),  # 256 experts, skewed: single- and multi-tile experts side by side
     (2, 1024, 256, 128, 8, 0.0),    # the most experts a plan takes (1024): decode kernels
+    (8, 8, 512, 256, 8, 0.0),       # decode kernels, every expert selected by every token (4 units each)
+    (6, 12, 768, 512, 4, 1.2),      # decode kernels, skewed: experts of 1-6 routes
     (600, 1024, 256, 128, 8, 0.5),  # 1024 experts on the route plan and the prefill kernels
 ])
 def test_routed_experts_matches_oracle(device, tokens, experts, hidden, inter, top_k, zipf):

@@ -264,3 +264,17 @@ def test_decode_kernels_take_at_most_64_routes():
     assert not uses_decode_kernels(9, 8, 512, 256)   # 72 routes: route plan + grouped GEMMs
     assert uses_decode_kernels(64, 1, 512, 256)
     assert not uses_decode_kernels(65, 1, 512, 256)
+
+
+def test_bench_reads_measured_traffic_from_the_profiles():
+    """bench.py's roofline `traffic` comes from the profiles/*_hbm_traffic.md
+    summaries (their `bench-traffic:` lines), one per measured config."""
+    import bench
+    from glm_moe import synthetic as S
+
+    found = bench.measured_traffic()
+    assert "decode_t1" in found
+    for name, rec in found.items():
+        base, _, mode = name.partition(":")
+        assert base in S.CONFIGS and mode in ("", "fp8"), name
+        assert rec["bytes"] > 0 and rec["source"].startswith("profiles/")
