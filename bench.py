@@ -667,11 +667,15 @@ def main():
         print(json.dumps({"error": "no GPU visible"}))
         sys.exit(1)
     device = torch.device("cuda:0")
-    cfg = S.CONFIGS[args.config]
+    base, _, mode = args.config.partition(":")
+    if mode not in ("", "fp8"):
+        raise SystemExit(f"unknown mode {mode!r}: a config takes no suffix or ':fp8'")
+    cfg = S.CONFIGS[base]
+    activations = "float8_e4m3fn" if mode == "fp8" else "bfloat16"
     print(f"[bench] generating {cfg.experts} experts of {cfg.name} weights on {device}", file=sys.stderr, flush=True)
     tables = S.device_expert_tables(cfg, seed=0, device=device)
     torch.cuda.synchronize()
-    work = Workload(cfg, tables, device)
+    work = Workload(cfg, tables, device, activations=activations)
     print(f"[bench] timing {args.steps} steps after {args.warmup} warmups", file=sys.stderr, flush=True)
     # headline: the K steps replayed from one HIP graph (the eager loop beside it);
     # per-kernel times: an eager loop with HIP events the kernels record on the
@@ -693,13 +697,13 @@ def main():
     with_full_layer(head, work, args.steps)
     with_router(head, cfg, device)
     with_mlp_from_logits(head, work, args.steps)
-    roofline = dominant_roofline(cfg, head)
+    roofline = dominant_roofline(cfg, head, mode)
     if args.copy_calibration:
         copy_calibration(device)
 
     secondary = {}
     for name in [s for s in args.secondary.split(",") if s]:
-        if name == cfg.name:
+        if name == args.config:
             continue
         base, _, mode = name.partition(":")
         scfg = S.CONFIGS[base]
@@ -722,7 +726,7 @@ def main():
 
     line = {
         "metric": "us per routed-expert MoE layer (decode T=1, E=256, H=6144, I=2048, top-8)"
-        if cfg.name == "decode_t1" else f"us per routed-expert MoE layer ({cfg.name})",
+        if args.config == "decode_t1" else f"us per routed-expert MoE layer ({args.config})",
         "value": head["us_per_layer"],
         "unit": "us/layer",
         "n_gpus": 1,
@@ -732,7 +736,7 @@ def main():
         "higher_is_better": False,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "bf16",
+        "dtype": "fp8 e4m3 x e4m3 (native FP8 mode)" if mode == "fp8" else "bf16",
         "data": "synthetic (seeded N(0,1) activations and router logits, N(0,0.02) e4m3fn weights with "
                 "128x128 FP32 block scales, generated on the GPU)",
         "config": {
