@@ -173,6 +173,7 @@ __device__ __forceinline__ int64_t out_row(const GroupedGemmArgs& a, int col, in
 }
 
 
+
 // 16 bytes a lane from rsrc + voffset + soffset straight into LDS at
 // lds + 16 * lane (buffer_load_dwordx4 ... lds).  The builtin only exists for
 // the device target; the host pass of the kernel template must not see it.
@@ -188,6 +189,65 @@ __device__ __forceinline__ void load_lds_16(__amdgpu_buffer_rsrc_t rsrc, uint8_t
 constexpr int kStripeBlockBytes = 32768;  // e4m3 bytes of 256 weight rows per K block
 constexpr int kTallBlockBytes = 65536;    // e4m3 bytes of 512 weight rows per K block
 constexpr int kPrefillLds = 160 * 1024;  // the whole LDS of a CU
+
+// The epilogue of a work item, through LDS: every wave writes its output
+// fragments (the epilogue's bf16 values: SwiGLU of the two tables, or the one
+// table rounded) into an image of the tile's route rows, OUT outputs each,
+// and the workgroup then stores every route row as 16-byte pieces, 8 lanes a
+// 128-byte line, so each line of the output is written whole by one
+// instruction, with the non-temporal hint (the rows are read once, by the
+// next kernel).  Stored straight from the MFMA layout (16 route rows x 32
+// bytes an instruction) with ordinary stores, each output line reached the
+// L2 as 32-byte pieces from four instructions of two waves, and the layer's
+// output writes slowed the weight stream that runs beside them: against a
+// timing variant whose stores stay in L2, T=2048 prefill was 7 % (bf16) and
+// 15 % (FP8 mode) slower.  Whole lines with the hint recover most of that
+// (T=2048 layer -2..-3 %, FP8 mode -8 %, T=8192 Zipf -2 %); whole lines
+// without it, or the hint on the scattered stores, do not.  Output column
+// of fragment (wave, rg, lane): n_item + wave * RGS * 16 + rg * 16 +
+// (lane / 16) * 4 .. + 3.  The caller has waited for its last direct-to-LDS
+// loads; the first barrier waits for every wave's last reads of the rings.
+template <int NCG, int RGS, int TABLES, int EPI, int WAVES>
+__device__ __forceinline__ void store_tile_lines(const GroupedGemmArgs& a, uint8_t* lds,
+                                                 const f32x4 (&acc)[TABLES][RGS][NCG], const int (&orow)[NCG],
+                                                 int live, int wave, int lane, int64_t n_item) {
+  static_assert(EPI == kEpiSwiglu || EPI == kEpiStoreBf16, "the prefill epilogues store bf16");
+  constexpr int OUT = WAVES * RGS * 16;  // outputs of one route row in this work item
+  constexpr int ROWS = NCG * 16;
+  constexpr int PITCH = OUT * 2 + 16;    // staged row bytes: +16 puts a fragment's 16 rows in distinct banks
+  constexpr int LPR = OUT * 2 / 16;      // 16-byte pieces of a route row
+  static_assert(ROWS * PITCH + ROWS * 4 <= kPrefillLds, "the staged tile fits the LDS");
+  static_assert((LPR & (LPR - 1)) == 0, "pieces per row: a power of two");
+  const int lrow = lane & 15, lgrp = lane >> 4;
+  int* const srow = reinterpret_cast<int*>(lds + ROWS * PITCH);
+  __syncthreads();  // every wave is done with the rings
+#pragma unroll
+  for (int cg = 0; cg < NCG; ++cg)
+#pragma unroll
+    for (int rg = 0; rg < RGS; ++rg) {
+      const f32x4& g = acc[0][rg][cg];
+      const f32x4& u = acc[TABLES - 1][rg][cg];
+      float v[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        v[j] = EPI == kEpiSwiglu ? swiglu_bf16(round_to_bf16(g[j]), round_to_bf16(u[j])) : g[j];
+      *reinterpret_cast<u32x2*>(lds + (cg * 16 + lrow) * PITCH + (wave * RGS * 16 + rg * 16 + lgrp * 4) * 2) =
+          u32x2{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+    }
+  if (wave == 0 && lgrp == 0) {
+#pragma unroll
+    for (int cg = 0; cg < NCG; ++cg) srow[cg * 16 + lrow] = (int)out_row(a, cg * 16 + lrow, live, orow[cg]);
+  }
+  __syncthreads();
+  uint16_t* const out = static_cast<uint16_t*>(a.out) + n_item;
+  for (int i = wave * 64 + lane; i < ROWS * LPR; i += WAVES * 64) {
+    const int r = i / LPR, part = i % LPR;
+    const int o = srow[r];
+    if (o >= 0)
+      __builtin_nontemporal_store(*reinterpret_cast<const u32x4*>(lds + r * PITCH + part * 16),
+                                  reinterpret_cast<u32x4*>(out + (int64_t)o * a.ldo + part * 8));
+  }
+}
 
 // Ring depths of one column-group variant, within 160 KB of LDS: SW weight
 // blocks of BLOCK bytes (every wave's rows of the stripe) and SX activation
@@ -316,13 +376,18 @@ __global__ __launch_bounds__(64 * WAVES, 1) void prefill_gemm_kernel(const Group
   }
   const int woff = (lane >> 3) * K + (((lane & 7) ^ (lane >> 3)) << 4);
   uint8_t* const wring = lds + wave * WAVE_BLOCK;  // ring slot s at + s * BLOCK
-  // A half stripe of a tall stripe (wide listings): RH row groups per table,
-  // GH weight groups a wave, half h's group gl being group
-  // (gl / RH) * RG + h * RH + gl % RH of the stripe; its ring has 32 KB slots,
-  // the wave's rows of slot s at lds + wave * GH * 2 KB + s * 32 KB.
+  // A half stripe of a tall stripe (wide listings): half h is rows
+  // h * BN / 2 .. (h + 1) * BN / 2 - 1 of each table of the stripe, so its
+  // outputs are one contiguous run of BN / 2 columns; RH row groups per table
+  // and GH weight groups a wave, group gl being table gl / RH, rows
+  // h * BN / 2 + wave * RH * 16 + (gl % RH) * 16 .. +15 (own descriptors and
+  // block scales); its ring has 32 KB slots, the wave's rows of slot s at
+  // lds + wave * GH * 2 KB + s * 32 KB.
   constexpr int RH = RG > 1 ? RG / 2 : 1;
   constexpr int GH = TABLES * RH;
   uint8_t* const hring = lds + wave * GH * 2048;
+  __amdgpu_buffer_rsrc_t hrsrc[GH];
+  float hscale[GH];
   // Weight blocks 0 and 1 (slots 0 and 1 of the variant's ring) go out before
   // the tile's rows are known: their HBM latency covers the tile and row-id
   // loads that the activation loads wait for.
@@ -337,16 +402,24 @@ __global__ __launch_bounds__(64 * WAVES, 1) void prefill_gemm_kernel(const Group
                                     blk < KB ? woff + 8 * h * K : kOutOfRange, blk < KB ? blk * kScaleBlock : 0);
   } else if constexpr (BLOCK > kStripeBlockBytes) {
 #pragma unroll
+    for (int gl = 0; gl < GH; ++gl) {
+      const int t = gl / RH;
+      const int rows = stripe * BN + wide_half * (BN / 2) + wave * RH * 16 + (gl % RH) * 16;
+      const uint8_t* wb = t == 0 ? a.w0 : a.w1;
+      const float* sb = t == 0 ? a.s0 : a.s1;
+      hrsrc[gl] = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(wb + ((size_t)e * N + rows) * (size_t)K),
+                                                    (short)0, 16 * K, kBufferFormat);
+      const float* srow = sb + ((size_t)e * (N / kScaleBlock) + rows / kScaleBlock) * KB;
+      hscale[gl] = lane < KB ? srow[lane] : 0.0f;
+    }
+#pragma unroll
     for (int blk = 0; blk < 2; ++blk)
 #pragma unroll
       for (int gl = 0; gl < GH; ++gl)
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
-          const int g0 = (gl / RH) * RG + gl % RH;
-          load_lds_16<kNonTemporal>(wide_half ? wrsrc[g0 + RH] : wrsrc[g0],
-                                    hring + blk * kStripeBlockBytes + (2 * gl + h) * 1024,
+        for (int h = 0; h < 2; ++h)
+          load_lds_16<kNonTemporal>(hrsrc[gl], hring + blk * kStripeBlockBytes + (2 * gl + h) * 1024,
                                     blk < KB ? woff + 8 * h * K : kOutOfRange, blk < KB ? blk * kScaleBlock : 0);
-        }
   }
   const int r0 = uniform(a.tile_row[tile]);
   const int tl = uniform(a.tile_live[tile]);
@@ -546,18 +619,10 @@ __global__ __launch_bounds__(64 * WAVES, 1) void prefill_gemm_kernel(const Group
         }
       }
     }
-    wait_all_loads();  // no load may still target LDS when the workgroup ends
+    wait_all_loads();  // the rings are idle: the epilogue reuses the LDS
 
     // Epilogue: lane holds rows n .. n+3 of route column cg*16 + lrow.
-    int64_t orow_ok[NCG];
-#pragma unroll
-    for (int cg = 0; cg < NCG; ++cg) orow_ok[cg] = out_row(a, cg * 16 + lrow, live, orow[cg]);
-#pragma unroll
-    for (int cg = 0; cg < NCG; ++cg)
-#pragma unroll
-      for (int rg = 0; rg < RG; ++rg)
-        store_fragment_at<TABLES, EPI>(a, orow_ok[cg], 1.0f, n0 + rg * 16 + lgrp * 4, acc[0][rg][cg],
-                                       acc[TABLES - 1][rg][cg]);
+    store_tile_lines<NCG, RG, TABLES, EPI, WAVES>(a, lds, acc, orow, live, wave, lane, (int64_t)stripe * BN);
   };
 
   // Tiles in half-block activation stages: the wide tiles (NCG = 10, 12, 14
@@ -623,20 +688,19 @@ __global__ __launch_bounds__(64 * WAVES, 1) void prefill_gemm_kernel(const Group
     load_out_rows(a, r0, live, lrow, orow);
 
     {
-      // the sub-stripe's weight groups: table gl / RS, rows n0 + (ss * RS +
-      // gl % RS) * 16 .. (their blocks 0 and 1 went out above in this layout)
+      // the sub-stripe's weight groups: the whole stripe's (SUB = 1), or the
+      // half stripe's (their blocks 0 and 1 went out above in this layout)
       const int ss = SUB == 1 ? 0 : wide_half;
       __amdgpu_buffer_rsrc_t wsub[GS];
       float ssc[GS];
 #pragma unroll
       for (int gl = 0; gl < GS; ++gl) {
-        const int g0 = (gl / RS) * RG + gl % RS;
         if constexpr (SUB == 1) {
-          wsub[gl] = wrsrc[g0];
-          ssc[gl] = sreg[g0];
+          wsub[gl] = wrsrc[gl];
+          ssc[gl] = sreg[gl];
         } else {
-          wsub[gl] = ss ? wrsrc[g0 + RS] : wrsrc[g0];
-          ssc[gl] = ss ? sreg[g0 + RS] : sreg[g0];
+          wsub[gl] = hrsrc[gl];
+          ssc[gl] = hscale[gl];
         }
       }
       // load j of half `part` of weight block blk's loads (group l / 2, rows 8 (l % 2) ..)
@@ -747,17 +811,10 @@ __global__ __launch_bounds__(64 * WAVES, 1) void prefill_gemm_kernel(const Group
         barrier();
         half_pass(std::integral_constant<int, 1>{});
       }
-      wait_all_loads();  // no load may still target LDS when the workgroup ends
+      wait_all_loads();  // the rings are idle: the epilogue reuses the LDS
 
-      int64_t orow_ok[NCG];
-#pragma unroll
-      for (int cg = 0; cg < NCG; ++cg) orow_ok[cg] = out_row(a, cg * 16 + lrow, live, orow[cg]);
-#pragma unroll
-      for (int cg = 0; cg < NCG; ++cg)
-#pragma unroll
-        for (int rg = 0; rg < RS; ++rg)
-          store_fragment_at<TABLES, EPI>(a, orow_ok[cg], 1.0f, n0 + (ss * RS + rg) * 16 + lgrp * 4,
-                                         acc[0][rg][cg], acc[TABLES - 1][rg][cg]);
+      store_tile_lines<NCG, RS, TABLES, EPI, WAVES>(a, lds, acc, orow, live, wave, lane,
+                                                    (int64_t)stripe * BN + ss * (BN / SUB));
     }
   };
   using I = std::integral_constant<int, 1>;
@@ -1274,16 +1331,8 @@ __global__ __launch_bounds__(64 * WAVES, 1) void prefill_gemm_fp8_kernel(const G
         }
       }
     }
-    wait_all_loads();  // no load may still target LDS when the workgroup ends
-    int64_t orow_ok[NCG];
-#pragma unroll
-    for (int cg = 0; cg < NCG; ++cg) orow_ok[cg] = out_row(a, cg * 16 + lrow, live, orow[cg]);
-#pragma unroll
-    for (int cg = 0; cg < NCG; ++cg)
-#pragma unroll
-      for (int rg = 0; rg < RG; ++rg)
-        store_fragment_at<TABLES, EPI>(a, orow_ok[cg], 1.0f, s0 * BN + wave * RG * 16 + rg * 16 + lgrp * 4,
-                                       acc[0][rg][cg], acc[TABLES - 1][rg][cg]);
+    wait_all_loads();  // the rings are idle: the epilogue reuses the LDS
+    store_tile_lines<NCG, RG, TABLES, EPI, WAVES>(a, lds, acc, orow, live, wave, lane, (int64_t)s0 * BN);
   };
   if constexpr (TALL) {
     switch (ncg) {
