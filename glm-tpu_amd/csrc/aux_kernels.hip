@@ -220,20 +220,11 @@ __global__ __launch_bounds__(256) void route_noaux_tc_kernel(const float* logits
   }
 }
 
-// Wave-wide maximum (every lane active), wave-uniform: DPP moves inside each
-// 16-lane row (quad lanes xor 1 and xor 2, then the half-row and row mirrors),
-// then the four row maxima through v_readlane -- no LDS round trip.  fmaxf
-// ignores a NaN operand, so the result does not depend on the pairing order.
-template <int CTRL>
-__device__ __forceinline__ float max_dpp(float v) {
-  return fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF,
-                                                                        0xF, false)));
-}
+// Wave-wide maximum (every lane active), wave-uniform: the 16-lane row maxima
+// by DPP moves (row16_max_f32), then the four of them through v_readlane -- no
+// LDS round trip.
 __device__ __forceinline__ float wave_max_f32(float v) {
-  v = max_dpp<0xB1>(v);   // quad_perm [1, 0, 3, 2]
-  v = max_dpp<0x4E>(v);   // quad_perm [2, 3, 0, 1]
-  v = max_dpp<0x141>(v);  // row_half_mirror
-  v = max_dpp<0x140>(v);  // row_mirror
+  v = row16_max_f32(v);
   const auto lane_value = [&](int l) { return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l)); };
   return fmaxf(fmaxf(lane_value(0), lane_value(16)), fmaxf(lane_value(32), lane_value(48)));
 }
@@ -272,14 +263,9 @@ __global__ __launch_bounds__(256) void quantize_rows_fp8_kernel(const uint16_t* 
 
 // The same with 16 lanes per (row, 128-wide K block): four blocks a wave, 8
 // values a lane (one 16-byte load, one 8-byte store), the block maximum over
-// the lane's 16-lane row by DPP moves (every lane of the row gets it).  Same
-// values, scales and NaN handling as quantize_rows_fp8_kernel.
-__device__ __forceinline__ float row16_max_f32(float v) {
-  v = max_dpp<0xB1>(v);   // quad_perm [1, 0, 3, 2]
-  v = max_dpp<0x4E>(v);   // quad_perm [2, 3, 0, 1]
-  v = max_dpp<0x141>(v);  // row_half_mirror
-  return max_dpp<0x140>(v);  // row_mirror
-}
+// the lane's 16-lane row by DPP moves (quantize_block16_fp8, which the FP8
+// prefill kernel's gate/up epilogue shares).  Same values, scales and NaN
+// handling as quantize_rows_fp8_kernel.
 __global__ __launch_bounds__(256) void quantize_rows_fp8_x8_kernel(const uint16_t* x, int64_t rows, int64_t k,
                                                                    uint8_t* q, float* scales,
                                                                    const int32_t* positions, int per_row,
@@ -297,17 +283,8 @@ __global__ __launch_bounds__(256) void quantize_rows_fp8_x8_kernel(const uint16_
       f[2 * j] = bf16_bits_to_f32(v[j] & 0xFFFFu);
       f[2 * j + 1] = bf16_bits_to_f32(v[j] >> 16);
     }
-    float a = 0.0f;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) a = fmaxf(a, fabsf(f[j]));
-    const float m = row16_max_f32(a);
-    const float scale = m > 0.0f ? m / 448.0f : 1.0f;
-    auto clamp448 = [](float t) { return t != t ? t : fminf(fmaxf(t, -448.0f), 448.0f); };
-    uint32_t w0 = 0, w1 = 0;
-    w0 = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(clamp448(f[0] / scale), clamp448(f[1] / scale), (int)w0, false);
-    w0 = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(clamp448(f[2] / scale), clamp448(f[3] / scale), (int)w0, true);
-    w1 = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(clamp448(f[4] / scale), clamp448(f[5] / scale), (int)w1, false);
-    w1 = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(clamp448(f[6] / scale), clamp448(f[7] / scale), (int)w1, true);
+    uint32_t w0, w1;
+    const float scale = quantize_block16_fp8(f, w0, w1);
     *reinterpret_cast<uint2*>(q + row * k + col) = make_uint2(w0, w1);
     for (int j = l16; j < per_row; j += 16) {
       const int64_t pos = positions != nullptr ? positions[row * per_row + j] : row;

@@ -433,6 +433,14 @@ int routed_experts_impl(const uint16_t* hidden, int64_t tokens, int64_t hidden_s
   g.tile_rows = tile_rows;
   g.wide_twice = p.wide_twice;
   g.tall = tall ? 1 : 0;
+  // FP8 mode on tall stripes: the gate/up epilogue quantises its SwiGLU rows
+  // for the down projection itself (the values the quantize launch below
+  // would write from the bf16 rows, which are then not written at all)
+  const bool fused_quant = fp8 && shape == kShapeWide && prefill_quantizes_output(g, 2, kEpiSwiglu);
+  if (fused_quant) {
+    g.outq = actq;
+    g.outq_scale = actscale;
+  }
   timer.arm(kStageGateUp);
   GLM_HIP(launch_grouped_gemm(g, shape, 2, kEpiSwiglu, stream), "gate/up launch");
   timer.done(kStageGateUp);
@@ -457,8 +465,9 @@ int routed_experts_impl(const uint16_t* hidden, int64_t tokens, int64_t hidden_s
   d.expert_first_tile = expert_first_tile;
   d.expert_tiles = expert_tiles;
   if (fp8) {
-    GLM_HIP(launch_quantize_rows_fp8(act, n, intermediate, actq, actscale, nullptr, 1, n, stream),
-            "quantize launch");
+    if (!fused_quant)
+      GLM_HIP(launch_quantize_rows_fp8(act, n, intermediate, actq, actscale, nullptr, 1, n, stream),
+              "quantize launch");
     d.xq = actq;
     d.xscale = actscale;
   }

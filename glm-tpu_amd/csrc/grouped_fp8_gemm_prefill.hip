@@ -239,6 +239,36 @@ __device__ __forceinline__ void store_tile_lines(const GroupedGemmArgs& a, uint8
     for (int cg = 0; cg < NCG; ++cg) srow[cg * 16 + lrow] = (int)out_row(a, cg * 16 + lrow, live, orow[cg]);
   }
   __syncthreads();
+  if constexpr (EPI == kEpiSwiglu && OUT % kScaleBlock == 0) {
+    if (a.outq != nullptr) {
+      // the rows quantised for the FP8 down projection: 16 lanes a (route row,
+      // 128-wide block), 8 values a lane, as launch_quantize_rows_fp8 does on
+      // the stored bf16 rows (quantize_block16_fp8); codes as whole 128-byte
+      // lines, scales block-major by output row
+      constexpr int NB = OUT / kScaleBlock;
+      const int l16 = lane & 15;
+      for (int i = wave * 4 + (lane >> 4); i < ROWS * NB; i += WAVES * 4) {
+        const int r = i / NB, b = i % NB;
+        const u32x4 v = *reinterpret_cast<const u32x4*>(lds + r * PITCH + (b * kScaleBlock + 8 * l16) * 2);
+        float f[8];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          f[2 * j] = bf16_bits_to_f32(v[j] & 0xFFFFu);
+          f[2 * j + 1] = bf16_bits_to_f32(v[j] >> 16);
+        }
+        uint32_t lo, hi;
+        const float scale = quantize_block16_fp8(f, lo, hi);
+        const int o = srow[r];
+        if (o >= 0) {
+          __builtin_nontemporal_store(u32x2{lo, hi},
+                                      reinterpret_cast<u32x2*>(a.outq + (int64_t)o * a.ldo + n_item + b * kScaleBlock +
+                                                               8 * l16));
+          if (l16 == 0) a.outq_scale[(n_item / kScaleBlock + b) * a.out_rows + o] = scale;
+        }
+      }
+      return;
+    }
+  }
   uint16_t* const out = static_cast<uint16_t*>(a.out) + n_item;
   for (int i = wave * 64 + lane; i < ROWS * LPR; i += WAVES * 64) {
     const int r = i / LPR, part = i % LPR;
@@ -1396,6 +1426,7 @@ int prefill_tall_bn(int tables) { return tables == 2 ? 8 * 32 : 8 * 64; }
 
 int prefill_stripe_run(int tables) { return tables == 2 ? kRunGateUp : kRunDown; }
 
+
 int prefill_wide_tile_rows() { return kBMWide; }
 
 // The prefill kernels hold one block scale per lane (K <= 64 blocks of 128).
@@ -1404,10 +1435,17 @@ bool prefill_fits(int64_t n, int64_t k, int tables) {
 }
 // Their activation buffer offsets are 32-bit: rows x K bf16 must stay below 2 GiB.
 bool prefill_rows_fit(int64_t x_rows, int64_t k) { return x_rows > 0 && x_rows * k * 2 <= INT32_MAX; }
+
+bool prefill_quantizes_output(const GroupedGemmArgs& a, int tables, int epilogue) {
+  return a.xq != nullptr && tables == 2 && epilogue == kEpiSwiglu && a.tall != 0 && a.n % prefill_tall_bn(2) == 0 &&
+         prefill_fits(a.n, a.k, 2) && prefill_rows_fit(a.x_rows, a.k);
+}
 hipError_t launch_grouped_gemm_prefill(const GroupedGemmArgs& a, int tables, int epilogue, hipStream_t stream) {
   if (a.max_tiles <= 0) return hipSuccess;
   if (a.expert_first_tile == nullptr || a.expert_tiles == nullptr) return hipErrorInvalidValue;
   if (!prefill_fits(a.n, a.k, tables) || !prefill_rows_fit(a.x_rows, a.k)) return hipErrorInvalidValue;
+  if ((a.outq != nullptr) != (a.outq_scale != nullptr)) return hipErrorInvalidValue;
+  if (a.outq != nullptr && !prefill_quantizes_output(a, tables, epilogue)) return hipErrorInvalidValue;
   if (a.xq != nullptr) {
     if (a.xscale == nullptr) return hipErrorInvalidValue;
     if (tables == 2 && epilogue == kEpiSwiglu)

@@ -74,4 +74,43 @@ __device__ __forceinline__ float swiglu_bf16(float g, float u) {
   return round_to_bf16(round_to_bf16(g * s) * u);
 }
 
+// max(v, v of the lane that DPP control CTRL names).  fmaxf ignores a NaN
+// operand, so a maximum built from these does not depend on the pairing order.
+template <int CTRL>
+__device__ __forceinline__ float max_dpp(float v) {
+  return fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF,
+                                                                        0xF, false)));
+}
+
+// Maximum over each 16-lane row of the wave (every lane of the row gets it):
+// quad lanes xor 1 and xor 2, then the half-row and row mirrors.
+__device__ __forceinline__ float row16_max_f32(float v) {
+  v = max_dpp<0xB1>(v);   // quad_perm [1, 0, 3, 2]
+  v = max_dpp<0x4E>(v);   // quad_perm [2, 3, 0, 1]
+  v = max_dpp<0x141>(v);  // row_half_mirror
+  return max_dpp<0x140>(v);  // row_mirror
+}
+
+// Activation quantisation of the native FP8 mode for one 128-value block held
+// by the 16 lanes of a 16-lane row, 8 values a lane: scale = amax / 448 (1 for
+// an all-zero block), q = e4m3fn(clamp(v / scale, +-448)) rounded to nearest
+// even (v_cvt_pk_fp8_f32), NaN stays NaN.  Returns the block's scale; the
+// lane's codes of values 0..3 in lo and 4..7 in hi (byte j = value j).
+__device__ __forceinline__ float quantize_block16_fp8(const float (&f)[8], uint32_t& lo, uint32_t& hi) {
+  float a = 0.0f;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) a = fmaxf(a, fabsf(f[j]));
+  const float m = row16_max_f32(a);
+  const float scale = m > 0.0f ? m / 448.0f : 1.0f;
+  auto clamp448 = [](float t) { return t != t ? t : fminf(fmaxf(t, -448.0f), 448.0f); };
+  uint32_t w0 = 0, w1 = 0;
+  w0 = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(clamp448(f[0] / scale), clamp448(f[1] / scale), (int)w0, false);
+  w0 = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(clamp448(f[2] / scale), clamp448(f[3] / scale), (int)w0, true);
+  w1 = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(clamp448(f[4] / scale), clamp448(f[5] / scale), (int)w1, false);
+  w1 = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(clamp448(f[6] / scale), clamp448(f[7] / scale), (int)w1, true);
+  lo = w0;
+  hi = w1;
+  return scale;
+}
+
 }  // namespace glm_moe

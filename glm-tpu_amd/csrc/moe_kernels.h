@@ -227,6 +227,12 @@ struct GroupedGemmArgs {
   int32_t wide_twice;          // the work list names tiles of more than 128 routes twice (RoutePlanArgs)
   int32_t tall;                // prefill kernels: tall stripes (512 weight rows) where N allows them
   const char* name;            // profiler base name (null: fp8_expert_panel_matmul)
+  // FP8 prefill kernel, SwiGLU epilogue on tall stripes (prefill_quantizes_output): nullable; the
+  // output rows quantised for the next projection instead of stored bf16 -- e4m3 codes
+  // [out_rows, ldo] and FP32 scales block-major by output row [n / 128][out_rows], the values of
+  // launch_quantize_rows_fp8 over the bf16 output
+  uint8_t* outq;
+  float* outq_scale;
 };
 
 // Profiler name of a grouped-GEMM launch: fp8_routed_projection_s{slots}_t{tables}
@@ -262,6 +268,9 @@ int prefill_tall_bn(int tables);
 int prefill_wide_tile_rows();
 // Weight stripes one FP8 prefill work item runs for a projection of `tables` tables.
 int prefill_stripe_run(int tables);
+// Whether launch_grouped_gemm_prefill on these args runs the FP8 kernel's tall
+// stripes with the SwiGLU epilogue, the launches that take GroupedGemmArgs::outq.
+bool prefill_quantizes_output(const GroupedGemmArgs& a, int tables, int epilogue);
 bool prefill_fits(int64_t n, int64_t k, int tables);
 // The prefill kernels' 32-bit activation offsets: x_rows x k x 2 bytes below 2 GiB.
 bool prefill_rows_fit(int64_t x_rows, int64_t k);
