@@ -161,11 +161,17 @@ class StageEvents:
         self._handles = []
 
 
-# One growable workspace buffer per (device, stream): calls enqueued on one
-# stream run in order, so they can share it; calls on different streams get
-# different buffers and never race.  A buffer grows to the largest call seen on
-# its stream and is kept until release_workspaces().  Calls captured into a HIP
-# graph take their own buffer from the graph's memory pool instead.
+# One growable workspace buffer per (device, stream) for the small (decode and
+# short-prefill) calls: calls enqueued on one stream run in order, so they can
+# share it; calls on different streams get different buffers and never race.
+# A buffer grows to the largest such call seen on its stream and is kept until
+# release_workspaces().  Workspaces above WORKSPACE_CACHE_MAX (long prefills:
+# ~270 MB at T=2048, ~1.3 GB at T=8192) are taken from torch's caching
+# allocator for the one call instead, so the memory goes back to torch's pool
+# (stream-ordered, for any tensor) when the call has been enqueued, rather than
+# staying held by this module; calls captured into a HIP graph take their own
+# buffer from the graph's memory pool.
+WORKSPACE_CACHE_MAX = 256 << 20
 _WORKSPACES: dict[tuple[int, int], torch.Tensor] = {}
 
 
@@ -176,10 +182,12 @@ def routed_workspace(tokens: int, top_k: int, num_experts: int, hidden: int, int
     nbytes = max(int(_lib.lib().glm_moe_routed_experts_workspace_bytes(
         tokens, top_k, num_experts, hidden, intermediate)), 1)
     device = torch.device(device)
-    if torch.cuda.is_current_stream_capturing():
+    if torch.cuda.is_current_stream_capturing() or nbytes > WORKSPACE_CACHE_MAX:
         # under HIP graph capture: a buffer of the graph's private memory pool,
         # which stays valid for every replay (a cached buffer could be regrown,
-        # and so freed, while the graph still uses it)
+        # and so freed, while the graph still uses it); above the cache's limit:
+        # torch's allocator, which reuses the block only for later work on this
+        # stream once the caller drops it
         return torch.empty(nbytes, dtype=torch.uint8, device=device)
     stream = torch.cuda.current_stream(device)
     key = (device.index if device.index is not None else torch.cuda.current_device(), stream.cuda_stream)

@@ -1444,3 +1444,26 @@ def test_prefill_layer_few_rows_uses_the_shared_rows_kernels(device, golden):
     other, _ = routed_experts(x, ids, w, *(t[k] for k in TABLE_KEYS), shared=_shared_swiglu(x, *shared),
                               routed_scale=2.5, check_weights=True)
     print("vs torch shared expert:", assert_moe_close(host_f32(out), host_f32(other)))
+
+
+def test_workspace_cache_keeps_small_and_releases_large(device):
+    """Small (decode) workspaces come from the per-stream cache; workspaces above
+    WORKSPACE_CACHE_MAX (long prefills) are torch allocations of the call alone
+    and are not held by the module."""
+    import importlib
+
+    from glm_moe import _lib
+
+    R = importlib.import_module("glm_moe.layers.moe.routed_experts")  # the module, not the function
+    R.release_workspaces()
+    small = R.routed_workspace(4, 8, 256, 6144, 2048, device)
+    again = R.routed_workspace(1, 8, 256, 6144, 2048, device)
+    assert again.data_ptr() == small.data_ptr() and len(R._WORKSPACES) == 1
+    big_bytes = int(_lib.lib().glm_moe_routed_experts_workspace_bytes(8192, 8, 256, 6144, 2048))
+    assert big_bytes > R.WORKSPACE_CACHE_MAX
+    big = R.routed_workspace(8192, 8, 256, 6144, 2048, device)
+    assert big.numel() == big_bytes and len(R._WORKSPACES) == 1
+    assert R._WORKSPACES[next(iter(R._WORKSPACES))].numel() < R.WORKSPACE_CACHE_MAX
+    del big
+    R.release_workspaces()
+    assert not R._WORKSPACES
