@@ -68,20 +68,21 @@ __device__ __forceinline__ float sigmoid_f32(float x) {
 
 // bf16(bf16(g * bf16(sigmoid(g))) * u) with g, u already bf16 values: the
 // SwiGLU of the reference with one bf16 rounding per elementwise op
-// (glm_tpu/layers/moe/routed_experts.py:102,280).  The sigmoid's division is
-// a reciprocal refined by one Newton step (a faithful FP32 quotient) except
-// where 1 + exp(-g) >= 2^126, whose quotient is an FP32 subnormal that the
-// reciprocal would flush: there the IEEE division.  bf16(sigmoid(g)) so
-// computed equals the IEEE quotient's for every bf16 g (all 65,536 checked on
-// the GPU), and bf16(g * s) is all of the sigmoid the later rounding sees.
+// (glm_tpu/layers/moe/routed_experts.py:102,280).  The sigmoid is
+// 1 / (1 + 2^(-g log2 e)) from the hardware exp2, its quotient a reciprocal
+// refined by one Newton step, except where 1 + exp(-g) >= 2^126, whose
+// quotient is an FP32 subnormal that the reciprocal would flush: there
+// 1 / (1 + expf(-g)) with the IEEE division.  bf16(sigmoid(g)) so computed
+// equals sigmoid_f32's for every bf16 g (all 65,536 checked on the GPU), and
+// bf16(g * s) is all of the sigmoid that the later rounding sees.
 __device__ __forceinline__ float swiglu_bf16(float g, float u) {
-  const float y = 1.0f + expf(-g);
+  const float y = 1.0f + __builtin_amdgcn_exp2f(g * -1.44269504088896341f);
   float q;
   if (__builtin_expect(y < 0x1p126f, 1)) {
     const float r = __builtin_amdgcn_rcpf(y);
     q = __builtin_fmaf(__builtin_fmaf(-y, r, 1.0f), r, r);
   } else {
-    q = 1.0f / y;
+    q = sigmoid_f32(g);
   }
   const float s = round_to_bf16(q);
   return round_to_bf16(round_to_bf16(g * s) * u);
