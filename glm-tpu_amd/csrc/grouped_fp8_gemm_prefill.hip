@@ -33,14 +33,16 @@
 //     activations in half K blocks.  On tall stripes a wide tile is listed
 //     twice by the plan and each listing takes one 256-row half of the
 //     stripe (the accumulators of all 512 rows would not fit in registers).
-// Work items are ordered expert-major, then in blocks of route tiles x
+// Work items are ordered expert-major, heaviest expert first (the plan lists
+// experts by route count, descending), then in blocks of route tiles x
 // stripes (item_of_expert), and dealt to the XCDs in chunks of 32 consecutive
 // items (one per CU of an XCD; workgroup b runs on XCD b % 8): chunk c goes to
-// XCD c % 8, so the tiles that share an expert's weight stripe (hot experts)
-// and the stripes that share a tile's activation rows run together on one XCD,
-// and every XCD gets its share of hot and cold experts (whole eighths of the
-// expert-major list left the XCD holding the cold tail idle for a third of a
-// T=8192 Zipf launch).
+// XCD c % 8 in even rounds of 8 chunks and 7 - c % 8 in odd ones (a snake), so
+// the tiles that share an expert's weight stripe (hot experts) and the stripes
+// that share a tile's activation rows run together on one XCD, and, the list
+// falling in cost, every XCD gets an even share of it (whole eighths of the
+// list left the XCD holding the cold tail idle for a third of a T=8192 Zipf
+// launch).
 #include <atomic>
 #include <type_traits>
 
@@ -62,14 +64,16 @@ constexpr int kXcds = 8;           // MI355X: 8 XCDs, workgroups dealt round-rob
 constexpr int kChunk = 32;         // work items dealt to an XCD together: one per CU
 
 // Work item of workgroup b (-1: none) when `total` items are dealt in chunks:
-// the q-th workgroup of XCD x = b % 8 runs item ((q / 32) * 8 + x) * 32 + q % 32.
-// Each XCD runs `per` workgroups, a whole number of chunks.
+// the q-th workgroup of XCD x = b % 8 runs item (j * 8 + x') * 32 + q % 32 with
+// j = q / 32 and x' = x for even j, 7 - x for odd j.  Each XCD runs `per`
+// workgroups, a whole number of chunks.
 __device__ __forceinline__ int xcd_item(int b, int total) {
   const int chunks = (total + kChunk - 1) / kChunk;
   const int per = (chunks + kXcds - 1) / kXcds * kChunk;
   const int q = b / kXcds;
   if (q >= per) return -1;
-  return ((q / kChunk) * kXcds + b % kXcds) * kChunk + q % kChunk;
+  const int j = q / kChunk, x = b % kXcds;
+  return (j * kXcds + ((j & 1) ? kXcds - 1 - x : x)) * kChunk + q % kChunk;
 }
 // Stripes one work item runs: a.stripe_run, clamped to 1 .. kMaxStripeRun,
 // and 1 when K has fewer than kMinRunBlocks blocks (the rings look up to 3

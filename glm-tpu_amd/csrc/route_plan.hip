@@ -49,6 +49,48 @@ __device__ int block_exclusive_scan(int v, int* scratch, int* total) {
   return r;
 }
 
+
+// First work-list index of this thread's expert when experts are listed
+// heaviest first (route count descending, ties by expert id): the tile list
+// then falls in cost, and the prefill kernels deal it to the XCDs in a snake
+// order, so that every XCD gets an even share of it.  c, nt: the routes and
+// tiles of expert threadIdx.x (0 past E); s_free: 3 * E ints of free LDS.
+// An expert's rank (its place in that order) is counted by `parts` threads,
+// each over every parts-th expert, and summed with LDS atomics.
+__device__ __forceinline__ int heavy_first_tile(int c, int nt, int E, int* s_free, int* s_scan, int* total) {
+  const int tid = threadIdx.x;
+  int* const s_cnt = s_free;           // [E] route counts, then list prefixes
+  int* const s_rank = s_free + E;      // [E] places in the heaviest-first order
+  int* const s_pos = s_free + 2 * E;   // [E] tiles of the expert at each place
+  __syncthreads();  // the caller's last reads of the LDS reused here
+  if (tid < E) {
+    s_cnt[tid] = c;
+    s_rank[tid] = 0;
+  }
+  __syncthreads();
+  const int parts = E <= kPlanThreads / 4 ? 4 : (E <= kPlanThreads / 2 ? 2 : 1);
+  const int i = tid / parts, part = tid % parts;
+  if (i < E) {
+    const int ci = s_cnt[i];
+    int r = 0;
+#pragma unroll 8
+    for (int j = part; j < E; j += parts) {
+      const int cj = s_cnt[j];
+      r += (cj > ci) | ((cj == ci) & (j < i));
+    }
+    atomicAdd(&s_rank[i], r);
+  }
+  __syncthreads();
+  const int rank = tid < E ? s_rank[tid] : 0;
+  if (tid < E) s_pos[rank] = nt;
+  __syncthreads();
+  const int v = tid < E ? s_pos[tid] : 0;
+  const int pre = block_exclusive_scan(v, s_scan, total);
+  if (tid < E) s_cnt[tid] = pre;  // the prefix of list place tid
+  __syncthreads();
+  return tid < E ? s_cnt[rank] : 0;
+}
+
 // Tiles listed for an expert of c routes: ceil(c / rows), plus (wide_twice)
 // a second listing of every tile of more than rows / 2 routes.
 __device__ __forceinline__ int tiles_of_count(int c, int rows, int wide_twice) {
@@ -194,12 +236,14 @@ __global__ __launch_bounds__(kPlanThreads) void route_plan_kernel(const RoutePla
   const bool bad = *s_bad != 0;
   if (tid == 0) a.valid[0] = bad ? 0 : 1;
 
-  // GEMM work list: ceil(count / tile_rows) tiles per expert, expert-major
+  // GEMM work list: ceil(count / tile_rows) tiles per expert, expert-major,
+  // heaviest expert first
   if (a.tile_rows > 0) {
     const int c = tid < E ? a.counts[tid] : 0;  // written above by this thread
     const int nt = tiles_of_count(c, a.tile_rows, a.wide_twice);
     int total = 0;
-    const int t0 = block_exclusive_scan(nt, s_scan, &total);
+    int* s_free = reinterpret_cast<int*>(s_pre);  // [kPlanWaves][ep] u16, free once the scatter is done  // [2][ep], free once the scatter is done
+    const int t0 = heavy_first_tile(c, nt, E, s_free, s_scan, &total);
     if (tid < E) {
       const int start = s_off[tid];
       if (a.expert_first_tile) a.expert_first_tile[tid] = t0;
@@ -395,7 +439,8 @@ __global__ __launch_bounds__(kPlanThreads) void route_scatter_kernel(const Route
     const int cnt = tid < E ? total_e : 0;
     const int nt = tiles_of_count(cnt, a.tile_rows, a.wide_twice);
     int tiles = 0;
-    const int t0 = block_exclusive_scan(nt, s_scan, &tiles);
+    int* s_free = reinterpret_cast<int*>(s_pre);  // [kPlanWaves][ep] u16, free once the scatter is done  // [2][ep], free once the scatter is done
+    const int t0 = heavy_first_tile(cnt, nt, E, s_free, s_scan, &tiles);
     if (tid < E) {
       const int start = ex;
       if (a.expert_first_tile) a.expert_first_tile[tid] = t0;
