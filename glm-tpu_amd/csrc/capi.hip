@@ -104,7 +104,7 @@ bool uses_decode_path(int64_t routes, int64_t hidden, int64_t intermediate) {
 
 // Byte layout of the glm_moe_routed_experts workspace.
 struct RoutedLayout {
-  size_t sorted, inverse, counts, offsets, tiles, expert_tiles, chunk_hist, chunk_bad, act, y, xq, xscale, actq,
+  size_t sorted, inverse, counts, offsets, tiles, tile_desc, chunk_hist, chunk_bad, act, y, xq, xscale, actq,
       actscale, act_shared, total;
   int64_t max_tiles;
 };
@@ -121,7 +121,7 @@ RoutedLayout routed_layout(int64_t tokens, int32_t top_k, int32_t experts, int64
   L.counts = off;  off = align_up(off + sizeof(int32_t) * experts);
   L.offsets = off; off = align_up(off + sizeof(int32_t) * (experts + 1));
   L.tiles = off;   off = align_up(off + sizeof(int32_t) * (3 * L.max_tiles + 1));
-  L.expert_tiles = off; off = align_up(off + sizeof(int32_t) * 2 * experts);
+  L.tile_desc = off; off = align_up(off + sizeof(int32_t) * 4 * L.max_tiles);
   // histogram rows of the plan (per chunk, or per router workgroup when the
   // router counts on the way): one sort key per expert, plus the key of unowned routes
   const int64_t hist_rows = route_plan_hist_rows(tokens, top_k);
@@ -268,8 +268,7 @@ int routed_experts_impl(const uint16_t* hidden, int64_t tokens, int64_t hidden_s
   int32_t* tile_row = tile_expert + L.max_tiles;
   int32_t* tile_live = tile_row + L.max_tiles;
   int32_t* tile_count = tile_live + L.max_tiles;
-  int32_t* expert_first_tile = reinterpret_cast<int32_t*>(ws + L.expert_tiles);
-  int32_t* expert_tiles = expert_first_tile + num_experts;
+  int32_t* tile_desc = reinterpret_cast<int32_t*>(ws + L.tile_desc);
   uint16_t* act = reinterpret_cast<uint16_t*>(ws + (compact_decode_scratch ? 0 : L.act));
   uint16_t* y = reinterpret_cast<uint16_t*>(ws + L.y);
   uint8_t* xq = reinterpret_cast<uint8_t*>(ws + L.xq);
@@ -373,8 +372,7 @@ int routed_experts_impl(const uint16_t* hidden, int64_t tokens, int64_t hidden_s
   p.tile_row = tile_row;
   p.tile_live = tile_live;
   p.tile_count = tile_count;
-  p.expert_first_tile = expert_first_tile;
-  p.expert_tiles = expert_tiles;
+  p.tile_desc = tile_desc;
   p.chunk_hist = reinterpret_cast<int32_t*>(ws + L.chunk_hist);
   p.chunk_bad = reinterpret_cast<int32_t*>(ws + L.chunk_bad);
   timer.arm(kStagePlan);
@@ -415,8 +413,7 @@ int routed_experts_impl(const uint16_t* hidden, int64_t tokens, int64_t hidden_s
   g.tile_live = tile_live;
   g.tile_count = tile_count;
   g.max_tiles = max_tiles;
-  g.expert_first_tile = expert_first_tile;
-  g.expert_tiles = expert_tiles;
+  g.tile_desc = tile_desc;
   if (fp8) {
     GLM_HIP(launch_quantize_rows_fp8(hidden, tokens, hidden_size, xq, xscale, inverse, top_k, n, stream),
             "quantize launch");
@@ -462,8 +459,7 @@ int routed_experts_impl(const uint16_t* hidden, int64_t tokens, int64_t hidden_s
   d.tile_live = tile_live;
   d.tile_count = tile_count;
   d.max_tiles = max_tiles;
-  d.expert_first_tile = expert_first_tile;
-  d.expert_tiles = expert_tiles;
+  d.tile_desc = tile_desc;
   if (fp8) {
     if (!fused_quant)
       GLM_HIP(launch_quantize_rows_fp8(act, n, intermediate, actq, actscale, nullptr, 1, n, stream),

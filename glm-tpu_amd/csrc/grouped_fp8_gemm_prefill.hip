@@ -125,6 +125,15 @@ constexpr int kRowBytes = kScaleBlock * 2;   // one staged activation row of a K
 // its rows, so a block holds 8 listings: again 4 tiles and ~32 / 4 half
 // stripes per 32 items.
 constexpr int kTileBlock = 4;
+// The FP8 kernel's tile blocks: 16 tiles of 128 routes, so a block of a hot
+// expert spans several chunks (XCDs), each running the 16 tiles over two runs
+// (GLM-5 shape on tall stripes: gate/up 8 runs, 4 chunks; down 12 runs, 6).
+// Its K loop takes half the bf16 kernel's time per weight byte, so the
+// re-reads of a hot expert's stripes by every tile block cost more: blocks of
+// 16 tiles read each stripe a quarter as often as blocks of 4, for more
+// activation reads (T=8192 Zipf FP8 layer -2..3 %; blocks of 8: -1.5 %; the
+// bf16 kernel gains nothing from larger blocks).
+constexpr int kTileBlockFp8 = 16;
 
 template <int TB = kTileBlock>
 __device__ __forceinline__ void item_of_expert(int rel, int runs, int nt, int& run, int& tile) {
@@ -137,6 +146,47 @@ __device__ __forceinline__ void item_of_expert(int rel, int runs, int nt, int& r
 }
 
 __device__ __forceinline__ void wait_all_loads() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+// The listings of the launch's work list, 0 when the plan reported bad routes
+// (the health byte read through its aligned dword, a scalar load; the count
+// stands in when there is no health byte).
+__device__ __forceinline__ int healthy_listings(const GroupedGemmArgs& a) {
+  const int mis = (int)(reinterpret_cast<uintptr_t>(a.valid) & 3);
+  const uint32_t* word = a.valid != nullptr ? reinterpret_cast<const uint32_t*>(a.valid - mis)
+                                            : reinterpret_cast<const uint32_t*>(a.tile_count);
+  const uint32_t health = *word;
+  const int listings = *a.tile_count;
+  return a.valid == nullptr || ((health >> (8 * mis)) & 0xFFu) != 0 ? listings : 0;
+}
+
+// A work item's expert from its listing's descriptor (expert e, first listing
+// t0, first sorted position, routes; RoutePlanArgs::tile_desc) -- one 16-byte
+// load -- and then its tile: listing rel of the expert's nt is tile rel
+// (rel / 2 when wide tiles are listed twice, the second listing when rel is
+// odd), the sorted rows r0 .. r0 + live - 1, exactly as the plan lists them.
+// False for a descriptor that cannot come from a consistent plan.
+struct ItemTile {
+  int e, t0, nt, start, count;  // the expert's
+  int half, live;               // the item's tile
+  int64_t r0;
+};
+__device__ __forceinline__ bool item_expert(const GroupedGemmArgs& a, int listing, ItemTile& t) {
+  listing = uniform(listing);
+  const int4 d = *reinterpret_cast<const int4*>(a.tile_desc + 4 * (int64_t)listing);
+  t.e = uniform(d.x);
+  t.t0 = uniform(d.y);
+  t.start = uniform(d.z);
+  t.count = uniform(d.w);
+  if (t.e < 0 || t.e >= a.experts || t.t0 < 0 || t.t0 > listing || t.start < 0 || t.count <= 0) return false;
+  t.nt = tiles_of_count(t.count, a.tile_rows, a.wide_twice);
+  return listing < t.t0 + t.nt;
+}
+__device__ __forceinline__ void item_place(const GroupedGemmArgs& a, int rel, ItemTile& t) {
+  const int j = a.wide_twice ? rel >> 1 : rel;
+  t.half = a.wide_twice ? rel & 1 : 0;
+  t.r0 = (int64_t)t.start + (int64_t)j * a.tile_rows;
+  t.live = min(a.tile_rows, t.count - j * a.tile_rows);
+}
 
 // This wave's loads but the newest N have completed (direct-to-LDS loads
 // included: their data is in LDS).  Unlike __syncthreads() the waits below
@@ -354,32 +404,42 @@ __global__ __launch_bounds__(64 * WAVES, 1) void prefill_gemm_kernel(const Group
   // [SW][WAVES][GROUPS][16 rows][128 B] weight ring, then [SX][NCG * 16 rows][256 B] activation ring
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
 
-  if (a.valid != nullptr && a.valid[0] == 0) return;
   const int stripes = a.n / BN;
-  const int total = stripes * a.tile_count[0];
+  const int total = stripes * healthy_listings(a);
   const int item = xcd_item(blockIdx.x, total);
   if (item < 0 || item >= total) return;
   // work-item scalars are workgroup-uniform: readfirstlane keeps them (and the
   // addresses derived from them) in scalar registers
-  const int e = uniform(a.tile_expert[item / stripes]);
-  if (e < 0 || e >= a.experts) return;
-  const int t0 = uniform(a.expert_first_tile[e]);
-  const int nt = uniform(a.expert_tiles[e]);
-  if (nt <= 0) return;
+  ItemTile it;
+  if (!item_expert(a, item / stripes, it)) return;
+  const int e = it.e, t0 = it.t0, nt = it.nt;
   int stripe, tile;
   item_of_expert<BLOCK == kStripeBlockBytes ? kTileBlock : 2 * kTileBlock>(item - stripes * t0, stripes, nt, stripe,
                                                                           tile);
+  item_place(a, tile, it);
   // On tall stripes with wide tiles listed twice, an expert's listings are
   // pairs (its wide tiles, the second listing taking the stripe's second
   // half), then at most one narrow tile: whether this item is a wide listing,
   // and of which half, follows from its place among the expert's nt listings
-  // -- before any tile metadata is loaded (checked against it below).
+  // (checked against the tile's route count below).
   int wide_half = -1;
   if constexpr (BLOCK > kStripeBlockBytes) {
     if (a.wide_twice != 0 && !((nt & 1) && tile == nt - 1)) wide_half = tile & 1;
   }
   tile += t0;
   if (stripe < 0 || stripe >= stripes || tile >= a.max_tiles) return;
+  // A wide tile listed twice: on tall stripes each listing takes one 256-row
+  // half of the stripe, as predicted above; 256-row stripes take the whole
+  // stripe on the first listing and skip the second.
+  const bool listing_ok = BLOCK == kStripeBlockBytes
+                              ? it.half == 0
+                              : (wide_half < 0 ? it.live <= kBM && it.half == 0
+                                               : it.live > kBM && it.half == wide_half);
+  // A consistent plan always passes; a corrupt one computes nothing instead of
+  // reading out of bounds.
+  if (it.live <= 0 || it.live > kBMWide || it.r0 + it.live > a.rows || !listing_ok) return;
+  const int r0 = (int)it.r0;
+  const int live = it.live;
 
   const int lane = threadIdx.x & 63;
   const int wave = uniform(threadIdx.x >> 6);
@@ -423,8 +483,8 @@ __global__ __launch_bounds__(64 * WAVES, 1) void prefill_gemm_kernel(const Group
   __amdgpu_buffer_rsrc_t hrsrc[GH];
   float hscale[GH];
   // Weight blocks 0 and 1 (slots 0 and 1 of the variant's ring) go out before
-  // the tile's rows are known: their HBM latency covers the tile and row-id
-  // loads that the activation loads wait for.
+  // the variant is chosen: their HBM latency covers the row-id loads that the
+  // activation loads wait for.
   if (wide_half < 0) {
 #pragma unroll
     for (int blk = 0; blk < 2; ++blk)
@@ -454,24 +514,6 @@ __global__ __launch_bounds__(64 * WAVES, 1) void prefill_gemm_kernel(const Group
         for (int h = 0; h < 2; ++h)
           load_lds_16<kNonTemporal>(hrsrc[gl], hring + blk * kStripeBlockBytes + (2 * gl + h) * 1024,
                                     blk < KB ? woff + 8 * h * K : kOutOfRange, blk < KB ? blk * kScaleBlock : 0);
-  }
-  const int r0 = uniform(a.tile_row[tile]);
-  const int tl = uniform(a.tile_live[tile]);
-  const int live = tl & kTileLiveMask;
-  // A wide tile listed twice (kTileSecondHalf on its second listing): on tall
-  // stripes each listing takes one 256-row half of the stripe, as predicted
-  // above; 256-row stripes take the whole stripe on the first listing and
-  // skip the second.
-  const int half = (tl & kTileSecondHalf) ? 1 : 0;
-  const bool listing_ok = BLOCK == kStripeBlockBytes
-                              ? half == 0
-                              : (wide_half < 0 ? live <= kBM && half == 0 : live > kBM && half == wide_half);
-  // A consistent plan always passes; a corrupt one computes nothing instead of
-  // reading out of bounds.
-  if (uniform(a.tile_expert[tile]) != e || r0 < 0 || live <= 0 || live > kBMWide || r0 + live > a.rows ||
-      (tl & ~(kTileLiveMask | kTileSecondHalf)) != 0 || !listing_ok) {
-    wait_all_loads();  // no load may still target LDS when the workgroup ends
-    return;
   }
   const int ncg = (live + 15) >> 4;
   const __amdgpu_buffer_rsrc_t xrsrc = __builtin_amdgcn_make_buffer_rsrc(
@@ -943,22 +985,25 @@ __global__ __launch_bounds__(64 * WAVES, 1) void prefill_gemm_fp8_kernel(const G
   // ring, [SX][128] FP32 activation-scale ring
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
 
-  if (a.valid != nullptr && a.valid[0] == 0) return;
   const int stripes = a.n / BN;
   const int R = TALL ? 1 : stripe_run_of(a);
   const int runs = (stripes + R - 1) / R;
-  const int total = runs * a.tile_count[0];
+  const int total = runs * healthy_listings(a);
   const int item = xcd_item(blockIdx.x, total);
   if (item < 0 || item >= total) return;
-  const int e = uniform(a.tile_expert[item / runs]);
-  if (e < 0 || e >= a.experts) return;
-  const int t0 = uniform(a.expert_first_tile[e]);
-  const int nt = uniform(a.expert_tiles[e]);
-  if (nt <= 0) return;
+  ItemTile it;
+  if (!item_expert(a, item / runs, it)) return;
+  const int e = it.e, t0 = it.t0, nt = it.nt;
   int run, tile;
-  item_of_expert(item - runs * t0, runs, nt, run, tile);
+  item_of_expert<kTileBlockFp8>(item - runs * t0, runs, nt, run, tile);
+  item_place(a, tile, it);
   tile += t0;
   if (run < 0 || run >= runs || tile >= a.max_tiles) return;
+  // A consistent plan always passes; a corrupt one computes nothing instead of
+  // reading out of bounds.
+  if (it.half != 0 || it.live <= 0 || it.live > kBM || it.r0 + it.live > a.rows) return;
+  const int r0 = (int)it.r0;
+  const int live = it.live;
   const int s0 = run * R;                // the run's first stripe
   const int nr = min(R, stripes - s0);   // and its stripe count
   const int lane = threadIdx.x & 63;
@@ -994,8 +1039,8 @@ __global__ __launch_bounds__(64 * WAVES, 1) void prefill_gemm_fp8_kernel(const G
   const int woff[2] = {(lane >> 3) * K + (((lane & 7) ^ row_swizzle(lane >> 3)) << 4),
                        (8 + (lane >> 3)) * K + (((lane & 7) ^ row_swizzle(8 + (lane >> 3))) << 4)};
   uint8_t* const wring = lds + wave * WAVE_BLOCK;  // ring slot s at + s * 32 KB
-  // the first stripe's weight blocks 0 and 1 go out before the tile metadata,
-  // as in the bf16 kernel
+  // the first stripe's weight blocks 0 and 1 go out before the row ids are
+  // read, as in the bf16 kernel
   {
     __amdgpu_buffer_rsrc_t w0r[GROUPS];
 #pragma unroll
@@ -1008,12 +1053,6 @@ __global__ __launch_bounds__(64 * WAVES, 1) void prefill_gemm_fp8_kernel(const G
         for (int h = 0; h < 2; ++h)
           load_lds_16<kNonTemporal>(w0r[g], wring + blk * BLOCK + (2 * g + h) * 1024,
                                     blk < KB ? woff[h] : kOutOfRange, blk < KB ? blk * kScaleBlock : 0);
-  }
-  const int r0 = uniform(a.tile_row[tile]);
-  const int live = uniform(a.tile_live[tile]);
-  if (uniform(a.tile_expert[tile]) != e || r0 < 0 || live <= 0 || live > kBM || r0 + live > a.rows) {
-    wait_all_loads();  // no load may still target LDS when the workgroup ends
-    return;
   }
   const int ncg = (live + 15) >> 4;
   auto phys_row = [&](int row) -> int64_t {
@@ -1446,7 +1485,10 @@ bool prefill_quantizes_output(const GroupedGemmArgs& a, int tables, int epilogue
 }
 hipError_t launch_grouped_gemm_prefill(const GroupedGemmArgs& a, int tables, int epilogue, hipStream_t stream) {
   if (a.max_tiles <= 0) return hipSuccess;
-  if (a.expert_first_tile == nullptr || a.expert_tiles == nullptr) return hipErrorInvalidValue;
+  if (a.tile_desc == nullptr || (reinterpret_cast<uintptr_t>(a.tile_desc) & 15) != 0 || a.tile_rows <= 0)
+    return hipErrorInvalidValue;
+  // the FP8 kernel's tiles: at most 128 routes, each listed once
+  if (a.xq != nullptr && (a.tile_rows > kBM || a.wide_twice != 0)) return hipErrorInvalidValue;
   if (!prefill_fits(a.n, a.k, tables) || !prefill_rows_fit(a.x_rows, a.k)) return hipErrorInvalidValue;
   if ((a.outq != nullptr) != (a.outq_scale != nullptr)) return hipErrorInvalidValue;
   if (a.outq != nullptr && !prefill_quantizes_output(a, tables, epilogue)) return hipErrorInvalidValue;

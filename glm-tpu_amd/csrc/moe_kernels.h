@@ -127,8 +127,8 @@ struct RoutePlanArgs {
   int32_t* tile_row;
   int32_t* tile_live;
   int32_t* tile_count;       // [1]
-  int32_t* expert_first_tile;  // nullable [experts]: first tile of each expert
-  int32_t* expert_tiles;       // nullable [experts]: tiles of each expert
+  int32_t* tile_desc;          // nullable [max_tiles][4], 16-byte aligned: per listing, its expert's
+                               // id, first listing, first sorted position and route count
   // optional scratch for the multi-workgroup plan (route_plan_chunks() chunks):
   int32_t* chunk_hist;         // [chunks, keys] key counts of each chunk
   int32_t* chunk_bad;          // [chunks] health of each chunk
@@ -139,6 +139,14 @@ struct RoutePlanArgs {
 // route count is tile_live & kTileLiveMask.
 constexpr int32_t kTileSecondHalf = 1 << 16;
 constexpr int32_t kTileLiveMask = kTileSecondHalf - 1;
+// Listings of an expert of c routes: ceil(c / rows) tiles, plus (wide_twice)
+// a second listing of every tile of more than rows / 2 routes -- then listing
+// i of the expert is tile i / 2, the second listing when i is odd.
+__host__ __device__ inline int tiles_of_count(int c, int rows, int wide_twice) {
+  const int full = c / rows, rem = c - full * rows;
+  const int nt = full + (rem > 0 ? 1 : 0);
+  return wide_twice ? nt + full + (rem > rows / 2 ? 1 : 0) : nt;
+}
 // Route chunks of the multi-workgroup plan (whole token rows, about 2048 routes each).
 constexpr int kPlanChunkRoutes = 2048;
 int route_plan_chunks(int32_t n, int32_t top_k);
@@ -212,8 +220,8 @@ struct GroupedGemmArgs {
   const int32_t* tile_live;
   const int32_t* tile_count;
   int32_t max_tiles;
-  const int32_t* expert_first_tile;  // prefill kernel: first work-list tile of each expert
-  const int32_t* expert_tiles;       // prefill kernel: work-list tiles of each expert
+  const int32_t* tile_desc;    // prefill kernels: the plan's per-listing expert descriptors
+                               // (RoutePlanArgs::tile_desc), with tile_rows and wide_twice
   const uint8_t* xq;           // nullable: e4m3 activations [x_rows, k] for the native FP8 mode
   const float* xscale;         // their FP32 block scales by sorted position [k / 128, rows]
   const uint8_t* valid;        // nullable: no work at all when *valid == 0
@@ -258,7 +266,7 @@ int gemm_shape_rows(int shape);
 int gemm_shape_bn(int shape, int tables);
 hipError_t launch_grouped_gemm_wide(const GroupedGemmArgs& a, int tables, int epilogue, hipStream_t stream);
 // The pipelined prefill kernel (expert-major XCD-aware work order); needs the
-// plan's expert_first_tile / expert_tiles.  Its bf16 kernel takes tiles of up
+// plan's tile_desc.  Its bf16 kernel takes tiles of up
 // to prefill_wide_tile_rows() routes, the FP8 kernel up to 128.  N must be a
 // multiple of prefill_bn(tables); both kernels run tall stripes of
 // prefill_tall_bn(tables) rows where GroupedGemmArgs::tall asks for them and

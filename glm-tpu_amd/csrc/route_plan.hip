@@ -91,16 +91,10 @@ __device__ __forceinline__ int heavy_first_tile(int c, int nt, int E, int* s_fre
   return tid < E ? s_cnt[rank] : 0;
 }
 
-// Tiles listed for an expert of c routes: ceil(c / rows), plus (wide_twice)
-// a second listing of every tile of more than rows / 2 routes.
-__device__ __forceinline__ int tiles_of_count(int c, int rows, int wide_twice) {
-  const int full = c / rows, rem = c - full * rows;
-  const int nt = full + (rem > 0 ? 1 : 0);
-  return wide_twice ? nt + full + (rem > rows / 2 ? 1 : 0) : nt;
-}
-
 // The work-list entries of expert e (c routes from sorted position start) from
-// list index t0 on, in route order; a second listing follows its tile.
+// list index t0 on, in route order; a second listing follows its tile.  With
+// a.tile_desc, each listing also gets the expert's descriptor {e, t0, start,
+// c}: a prefill work item places its tile from that one 16-byte read.
 __device__ __forceinline__ void write_tiles(const RoutePlanArgs& a, int e, int start, int c, int t0) {
   int idx = t0;
   for (int j = 0; j * a.tile_rows < c; ++j) {
@@ -111,6 +105,7 @@ __device__ __forceinline__ void write_tiles(const RoutePlanArgs& a, int e, int s
         a.tile_expert[idx] = e;
         a.tile_row[idx] = start + j * a.tile_rows;
         a.tile_live[idx] = live | (h ? kTileSecondHalf : 0);
+        if (a.tile_desc) *reinterpret_cast<int4*>(a.tile_desc + 4 * (int64_t)idx) = make_int4(e, t0, start, c);
       }
     }
   }
@@ -246,8 +241,6 @@ __global__ __launch_bounds__(kPlanThreads) void route_plan_kernel(const RoutePla
     const int t0 = heavy_first_tile(c, nt, E, s_free, s_scan, &total);
     if (tid < E) {
       const int start = s_off[tid];
-      if (a.expert_first_tile) a.expert_first_tile[tid] = t0;
-      if (a.expert_tiles) a.expert_tiles[tid] = nt;
       write_tiles(a, tid, start, c, t0);
     }
     // An invalid route set is still planned with its safe ids (invalid -> 0),
@@ -443,8 +436,6 @@ __global__ __launch_bounds__(kPlanThreads) void route_scatter_kernel(const Route
     const int t0 = heavy_first_tile(cnt, nt, E, s_free, s_scan, &tiles);
     if (tid < E) {
       const int start = ex;
-      if (a.expert_first_tile) a.expert_first_tile[tid] = t0;
-      if (a.expert_tiles) a.expert_tiles[tid] = nt;
       write_tiles(a, tid, start, cnt, t0);
     }
     if (tid == 0) a.tile_count[0] = min(tiles, a.max_tiles);
