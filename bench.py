@@ -62,6 +62,10 @@ def parse_args():
                         "numerics; ':share8' times the eight expert-parallel shares of the layer one by one")
     p.add_argument("--secondary-steps", type=int, default=20)
     p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--headline-only", action="store_true",
+                   help="time the headline config's routed layer alone (no full-layer, router or "
+                        "MLP-from-logits figures): in a rocprofv3 run, the kernels replayed from HIP graphs "
+                        "(listed under their symbol names) are then the routed layer's only")
     p.add_argument("--copy-calibration", action="store_true",
                    help="after the headline, copy a 1 GiB device buffer 3 times (the known-size kernel that "
                         "scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings)")
@@ -694,9 +698,10 @@ def main():
     head["us_per_layer_eager"] = ms_eager * 1e3
     head["us_per_layer_with_stage_events"] = ms_ev * 1e3
 
-    with_full_layer(head, work, args.steps)
-    with_router(head, cfg, device)
-    with_mlp_from_logits(head, work, args.steps)
+    if not args.headline_only:
+        with_full_layer(head, work, args.steps)
+        with_router(head, cfg, device)
+        with_mlp_from_logits(head, work, args.steps)
     roofline = dominant_roofline(cfg, head, mode)
     if args.copy_calibration:
         copy_calibration(device)
@@ -748,7 +753,7 @@ def main():
         "full_layer_us": head.get("full_layer_us"),
         "full_layer_hbm_gbs": head.get("full_layer_hbm_gbs"),
         "full_layer_note": head.get("full_layer_note", head.get("full_layer_error")),
-        "router": head["router"],
+        "router": head.get("router"),
         "mlp_from_logits": head.get("mlp_from_logits"),
         "layer_hbm_gbs": head["layer_hbm_gbs"],
         "layer_hbm_frac": head["layer_hbm_gbs"] / HBM_PEAK_GBS,
