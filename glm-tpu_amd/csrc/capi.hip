@@ -5,6 +5,7 @@
 #include <stdarg.h>
 #include <stdio.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstring>
 #include <mutex>
@@ -100,6 +101,22 @@ int64_t max_tiles_for(int64_t routes, int32_t experts, int rows) {
 // Routed-expert calls of at most 64 routes take the two-kernel decode path.
 bool uses_decode_path(int64_t routes, int64_t hidden, int64_t intermediate) {
   return routes <= kMaxDecodeRoutes && decode_path_fits(hidden, intermediate);
+}
+
+// Whether the bf16 down projection keeps tall stripes (512 weight rows a work
+// item) for about `listings` route tiles: unless its work items would leave
+// most CUs of the last round idle where 256-row stripes (twice the items)
+// fill the rounds -- an expert-parallel share's few experts (32 tiles x 12
+// tall stripes = 384 items on 256 CUs: 1.5 rounds).
+bool down_tall_fills(int64_t listings, int64_t hidden) {
+  int dev = 0, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) !=
+                                               hipSuccess || cus <= 0)
+    return true;
+  auto fill = [&](int64_t items) { return (double)items / (double)(((items + cus - 1) / cus) * cus); };
+  const int64_t tall_items = listings * (hidden / prefill_tall_bn(1));
+  const int64_t short_items = listings * (hidden / prefill_bn(1));
+  return !(fill(tall_items) < 0.85 && fill(short_items) > fill(tall_items) + 0.1);
 }
 
 // Byte layout of the glm_moe_routed_experts workspace.
@@ -476,7 +493,12 @@ int routed_experts_impl(const uint16_t* hidden, int64_t tokens, int64_t hidden_s
   d.stripe_run = prefill_stripe_run(1);
   d.tile_rows = tile_rows;
   d.wide_twice = p.wide_twice;
-  d.tall = tall ? 1 : 0;
+  // about one tile per expert of the call, or its share of the routes in whole tiles
+  // (wide tiles counted as their two listings)
+  const int64_t listing_rows = p.wide_twice ? tile_rows / 2 : tile_rows;
+  const int64_t listings_est =
+      std::max<int64_t>(num_experts, (n * num_experts / global_experts + listing_rows - 1) / listing_rows);
+  d.tall = tall && (fp8 || down_tall_fills(listings_est, hidden_size)) ? 1 : 0;
   timer.arm(kStageDown);
   GLM_HIP(launch_grouped_gemm(d, shape, 1, kEpiStoreBf16, stream), "down launch");
   timer.done(kStageDown);
