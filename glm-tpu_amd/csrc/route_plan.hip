@@ -49,7 +49,6 @@ __device__ int block_exclusive_scan(int v, int* scratch, int* total) {
   return r;
 }
 
-
 // First work-list index of this thread's expert when experts are listed
 // heaviest first (route count descending, ties by expert id): the tile list
 // then falls in cost, and the prefill kernels deal it to the XCDs in a snake
@@ -237,7 +236,7 @@ __global__ __launch_bounds__(kPlanThreads) void route_plan_kernel(const RoutePla
     const int c = tid < E ? a.counts[tid] : 0;  // written above by this thread
     const int nt = tiles_of_count(c, a.tile_rows, a.wide_twice);
     int total = 0;
-    int* s_free = reinterpret_cast<int*>(s_pre);  // [kPlanWaves][ep] u16, free once the scatter is done  // [2][ep], free once the scatter is done
+    int* s_free = reinterpret_cast<int*>(s_pre);  // [kPlanWaves][ep] u16, free once the scatter is done
     const int t0 = heavy_first_tile(c, nt, E, s_free, s_scan, &total);
     if (tid < E) {
       const int start = s_off[tid];
@@ -432,7 +431,7 @@ __global__ __launch_bounds__(kPlanThreads) void route_scatter_kernel(const Route
     const int cnt = tid < E ? total_e : 0;
     const int nt = tiles_of_count(cnt, a.tile_rows, a.wide_twice);
     int tiles = 0;
-    int* s_free = reinterpret_cast<int*>(s_pre);  // [kPlanWaves][ep] u16, free once the scatter is done  // [2][ep], free once the scatter is done
+    int* s_free = reinterpret_cast<int*>(s_pre);  // [kPlanWaves][ep] u16, free once the scatter is done
     const int t0 = heavy_first_tile(cnt, nt, E, s_free, s_scan, &tiles);
     if (tid < E) {
       const int start = ex;
