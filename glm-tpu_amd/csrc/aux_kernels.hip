@@ -119,18 +119,39 @@ __global__ void combine_routes_kernel(const uint16_t* y, int64_t tokens, int32_t
     const int64_t t = i / groups;
     const int64_t c = (i - t * groups) * 8;
     float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    {
-      for (int s = 0; s < top_k; ++s) {
-        if (ids != nullptr && owned_expert(ids[t * top_k + s], own) < 0) continue;  // not computed here
-        const u32x4 v = *reinterpret_cast<const u32x4*>(y + ((t * top_k + s) * h + c));
+    // the token's slots eight at a time: the slots computed here (another
+    // share's routes are skipped) are listed first, then their rows are all
+    // loaded before any is summed, so the loads overlap instead of each
+    // waiting behind its slot's ownership test
+    for (int s0 = 0; s0 < top_k; s0 += 8) {
+      int id[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) id[u] = ids != nullptr ? ids[t * top_k + min(s0 + u, top_k - 1)] : 0;
+      int slot[8];
+      int n = 0;
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+        if (s0 + u < top_k && (ids == nullptr || owned_expert(id[u], own) >= 0)) slot[n++] = s0 + u;
+      u32x4 v[8];
+      float w[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        if (u < n) {
+          v[u] = *reinterpret_cast<const u32x4*>(y + ((t * top_k + slot[u]) * h + c));
+          w[u] = route_w != nullptr ? route_w[t * top_k + slot[u]] : 1.0f;
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        if (u >= n) break;
         // bf16 route weight (routed_experts.py:104-105): bf16(bf16(down) * bf16(w))
-        const float w = route_w != nullptr ? round_to_bf16(route_w[t * top_k + s]) : 1.0f;
+        w[u] = round_to_bf16(w[u]);
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          float lo = bf16_bits_to_f32(v[j] & 0xFFFFu), hi = bf16_bits_to_f32(v[j] >> 16);
+          float lo = bf16_bits_to_f32(v[u][j] & 0xFFFFu), hi = bf16_bits_to_f32(v[u][j] >> 16);
           if (route_w != nullptr) {
-            lo = round_to_bf16(lo * w);
-            hi = round_to_bf16(hi * w);
+            lo = round_to_bf16(lo * w[u]);
+            hi = round_to_bf16(hi * w[u]);
           }
           acc[2 * j] += lo;
           acc[2 * j + 1] += hi;
