@@ -479,6 +479,8 @@ def _small_case(tokens, experts, hidden, inter, top_k, zipf, seed):
     (8, 8, 512, 256, 8, 0.0),       # decode kernels, every expert selected by every token (4 units each)
     (6, 12, 768, 512, 4, 1.2),      # decode kernels, skewed: experts of 1-6 routes
     (600, 1024, 256, 128, 8, 0.5),  # 1024 experts on the route plan and the prefill kernels
+    (700, 384, 256, 128, 8, 0.8),   # 384 experts: the plan ranks experts two threads apiece, skewed ties
+    (200, 300, 256, 128, 8, 0.0),   # 300 experts on the one-workgroup plan (1600 routes)
 ])
 def test_routed_experts_matches_oracle(device, tokens, experts, hidden, inter, top_k, zipf):
     from glm_moe.layers.moe.routed_experts import routed_experts
